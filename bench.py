@@ -1,0 +1,261 @@
+"""Benchmark of the decode hot path on one MI355X (BASELINE.json's metric and configs).
+
+A step is one Llama-3-8B decode layer at batch 1 through the hot path: the seven projections
+(q/o 4096x4096, k/v 1024x4096, gate/up 14336x4096, down 4096x14336) as four launches (q, k, v
+grouped; o; gate, up grouped; down), then one launch of the trusted blocked checker over all
+seven outputs at block b = 128, K = 1.  Weights are random (the reference's generator:
+N(0, 0.02) BF16, x ~ N(0, 1) BF16) and rotate over several distinct layer copies whose total
+exceeds L2 + MALL, so every step streams its weights from HBM, as decoding through a model does.
+
+Printed JSON line:
+  value          GEMV algorithmic bytes per step / time per step, checker included (GB/s)
+  roofline       the dominant kernel (the BF16 tree GEMV instance used by q/k/v, o, gate/up):
+                 algorithmic bytes per launch / its mean launch duration from HIP events
+                 recorded around each launch on the launch stream, against 8 TB/s
+  cpu_baseline   the oracle's CPU model of the same work (coalesced-tree GEMV + CPU blocked
+                 checker) timed on this host on a bounded sample
+plus the FP8 layer, GEMV-only times, the checker overhead and a read-only stream ceiling.
+
+Run: python bench.py [--gpus 1] [--steps 200] [--warmup 20]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "proof-carrying-kernels_amd"))
+
+HBM_PEAK_GBPS = 8000.0  # MI355X published HBM3E bandwidth
+LAYER = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+         ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]  # fmt: skip
+LAUNCHES = [("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up")), ("down", ("down",))]
+THREADS = 256
+BLOCK = 128
+
+
+def gemv_bytes(m: int, n: int, weight_bytes: int) -> int:
+    """Algorithmic bytes of one GEMV: weights, x (BF16) and y (FP32), the reference's formula
+    (harness/bench_gemv.py:74, harness/bench_fp8.py:56)."""
+    return weight_bytes * m * n + 2 * n + 4 * m
+
+
+def build_layers(copies: int, fp8: bool, gen):  # type: ignore[no-untyped-def]
+    import torch
+
+    from pck.cuda import GpuBlockedChecker, quantize_fp8
+    from pck.fp import tree_height
+
+    layers = []
+    for _ in range(copies):
+        layer = {}
+        for name, m, n in LAYER:
+            W = (torch.randn(m, n, generator=gen) * 0.02).to(torch.bfloat16)
+            x = torch.randn(n, generator=gen).to(torch.bfloat16).cuda()
+            Wd = W.cuda()
+            if fp8:
+                Q, _ = quantize_fp8(Wd)
+                checker = GpuBlockedChecker(Q.to(torch.bfloat16), BLOCK, tree_height(n, THREADS, 16), generator=gen)
+                layer[name] = (Q, x, checker)
+                del Wd
+            else:
+                checker = GpuBlockedChecker(Wd, BLOCK, tree_height(n, THREADS, 8), generator=gen)
+                layer[name] = (Wd, x, checker)
+        layers.append(layer)
+    return layers
+
+
+def run_step(layer, with_check: bool, events=None):  # type: ignore[no-untyped-def]
+    """One decode layer; with ``events`` a list that receives (launch, start, end) per launch."""
+    import torch
+
+    from pck.cuda import check_many, gemv_group
+
+    outs = {}
+    for launch, names in LAUNCHES:
+        if events is not None:
+            start = torch.cuda.Event(enable_timing=True)
+            start.record()
+        ys = gemv_group([(layer[n][0], layer[n][1]) for n in names], THREADS)
+        if events is not None:
+            end = torch.cuda.Event(enable_timing=True)
+            end.record()
+            events.append((launch, start, end))
+        outs.update(zip(names, ys))
+    if with_check:
+        if events is not None:
+            start = torch.cuda.Event(enable_timing=True)
+            start.record()
+        results = check_many([(layer[n][2], layer[n][1], outs[n]) for n, _, _ in LAYER])
+        if events is not None:
+            end = torch.cuda.Event(enable_timing=True)
+            end.record()
+            events.append(("check", start, end))
+        return outs, results
+    return outs, None
+
+
+def timed(layers, steps: int, warmup: int, with_check: bool, per_kernel: bool):  # type: ignore[no-untyped-def]
+    """(ms per step, {launch: [ms per launch]}) over ``steps`` steps after ``warmup``."""
+    import torch
+
+    for i in range(warmup):
+        run_step(layers[i % len(layers)], with_check)
+    events: list = [] if per_kernel else None  # type: ignore[assignment]
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        run_step(layers[i % len(layers)], with_check, events)
+    end.record()
+    torch.cuda.synchronize()
+    per_launch: dict[str, list[float]] = {}
+    for name, s, e in events or []:
+        per_launch.setdefault(name, []).append(s.elapsed_time(e))
+    return start.elapsed_time(end) / steps, per_launch
+
+
+def cpu_baseline() -> dict:
+    """The oracle on this host: the coalesced-tree CPU model of the q projection (4096 x 4096,
+    T = 256) plus the CPU blocked checker at b = 128, K = 1, median of 5 runs; GB/s of the same
+    metric (GEMV algorithmic bytes / time).  NumPy elementwise work is single-threaded; the
+    checker's matmuls use the BLAS threads."""
+    import numpy as np
+
+    from oracle.checker import BlockedChecker
+    from oracle.gemv import emulate_gemv_coalesced
+    from pck.fp import bf16, tree_height
+
+    m = n = 4096
+    rng = np.random.default_rng(0)
+    W = bf16(rng.standard_normal((m, n)) * 0.02)
+    x = bf16(rng.standard_normal(n))
+    times = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        y = emulate_gemv_coalesced(W, x, THREADS)
+        ok = BlockedChecker(W, x, BLOCK, tree_height(n, THREADS, 8)).verdict(y, rng, checks=1)
+        times.append(time.perf_counter() - t0)
+        assert ok.all()
+    t = statistics.median(times)
+    return {
+        "value": round(gemv_bytes(m, n, 2) / t / 1e9, 3),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": "oracle emulate_gemv_coalesced + BlockedChecker.verdict (K=1, b=128) on "
+        f"q 4096x4096, median of 5 runs ({t * 1e3:.0f} ms each), host has {os.cpu_count()} CPUs",
+    }
+
+
+def main() -> None:
+    parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--copies", type=int, default=4, help="distinct layer copies (> MALL)")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the decode hot path "
+              "here has no multi-GPU step", file=sys.stderr)  # fmt: skip
+        sys.exit(2)
+
+    import torch
+
+    from pck.cuda.timing import read_bandwidth_gbps
+
+    gen = torch.Generator().manual_seed(0)
+    print(f"[bench] building {args.copies} BF16 layer copies", file=sys.stderr, flush=True)
+    bf16_layers = build_layers(args.copies, fp8=False, gen=gen)
+    bytes_bf16 = sum(gemv_bytes(m, n, 2) for _, m, n in LAYER)
+    launch_bytes = {
+        launch: sum(gemv_bytes(m, n, 2) for name, m, n in LAYER if name in names)
+        for launch, names in LAUNCHES
+    }
+    # correctness first: every check passes on the honest outputs
+    _, results = run_step(bf16_layers[0], True)
+    assert all(bool(r.verdict.all()) for r in results), "checker rejected an honest output"
+
+    print("[bench] timing BF16 layer", file=sys.stderr, flush=True)
+    ms_checked, per_launch = timed(bf16_layers, args.steps, args.warmup, True, per_kernel=True)
+    ms_events_free, _ = timed(bf16_layers, args.steps, args.warmup, True, per_kernel=False)
+    ms_gemv_only, _ = timed(bf16_layers, args.steps, args.warmup, False, per_kernel=False)
+    del bf16_layers
+    torch.cuda.empty_cache()
+
+    print("[bench] building and timing FP8 layer", file=sys.stderr, flush=True)
+    fp8_layers = build_layers(args.copies, fp8=True, gen=gen)
+    _, results = run_step(fp8_layers[0], True)
+    assert all(bool(r.verdict.all()) for r in results), "checker rejected an honest FP8 output"
+    bytes_fp8 = sum(gemv_bytes(m, n, 1) for _, m, n in LAYER)
+    fp8_checked, fp8_launch = timed(fp8_layers, args.steps, args.warmup, True, per_kernel=True)
+    fp8_gemv_only, _ = timed(fp8_layers, args.steps, args.warmup, False, per_kernel=False)
+    del fp8_layers
+    torch.cuda.empty_cache()
+
+    read_ceiling = read_bandwidth_gbps()
+
+    # Dominant kernel: the BF16 tree GEMV instance of the n = 4096 launches (q/k/v, o, gate/up).
+    dom = ("qkv", "o", "gate_up")
+    dom_ms = [t for name in dom for t in per_launch[name]]
+    dom_bytes = sum(launch_bytes[name] * len(per_launch[name]) for name in dom)
+    achieved = dom_bytes / (sum(dom_ms) / 1e3) / 1e9
+    value = bytes_bf16 / (ms_events_free / 1e3) / 1e9
+
+    line = {
+        "metric": "GEMV HBM GB/s (% of peak), BF16/FP8, Llama-3-8B shapes; checker overhead %",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_events_free, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 x bf16 -> fp32 (checker fp64)",
+        "data": "synthetic: reference generator, W ~ N(0, 0.02) bf16, x ~ N(0, 1) bf16",
+        "config": {
+            "workload": "Llama-3-8B decode layer, batch 1: 7 BF16 GEMVs (4 launches) + 1 "
+            "blocked-checker launch, b=128, K=1, T=256",
+            "layer_copies": args.copies,
+            "gemv_bytes_per_step": bytes_bf16,
+        },
+        "pct_of_peak": round(100 * value / HBM_PEAK_GBPS, 2),
+        "gemv_only_gbps": round(bytes_bf16 / (ms_gemv_only / 1e3) / 1e9, 1),
+        "checker_overhead_pct": round(100 * (ms_events_free / ms_gemv_only - 1), 2),
+        "fp8": {
+            "value_gbps": round(bytes_fp8 / (fp8_checked / 1e3) / 1e9, 1),
+            "gemv_only_gbps": round(bytes_fp8 / (fp8_gemv_only / 1e3) / 1e9, 1),
+            "checker_overhead_pct": round(100 * (fp8_checked / fp8_gemv_only - 1), 2),
+            "ms_per_step": round(fp8_checked, 5),
+            "launch_ms": {k: round(statistics.mean(v), 5) for k, v in fp8_launch.items()},
+        },
+        "launch_ms": {k: round(statistics.mean(v), 5) for k, v in per_launch.items()},
+        "hbm_read_ceiling_gbps": round(read_ceiling, 1),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "gemv_tree_kernel<256,1,2,bf16> (q/k/v, o, gate/up launches)",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        print("[bench] timing the CPU baseline", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,140 @@
+/* C ABI of libpck_hip.so: the MI355X (gfx950) decode hot path of proof-carrying-kernels.
+ *
+ * Every entry point only enqueues work on `stream` (a hipStream_t passed as void*; NULL is the
+ * device's null stream) and returns a hipError_t value (0 = hipSuccess).  None allocates, frees,
+ * synchronises or reads device memory on the host.  All pointers are device pointers to
+ * contiguous arrays; the caller owns every buffer (outputs, scratch and banks included).
+ *
+ * Numerics (what the tests pin):
+ *   - the GEMVs reproduce the reference's summation trees bit for bit: lane t of `threads` virtual
+ *     lanes sums vectors t, t + threads, ... of 8 (BF16) or 16 (FP8) columns, starting from its
+ *     first product with columns past n as +0, then halving within 32-lane virtual warps and
+ *     across warp sums (tree height (vec * ceil(ceil(n / vec) / threads) - 1) + log2 threads);
+ *   - the checker evaluates rho = c.x - r.y and the threshold tau with every operation of tau
+ *     rounded up, and passes a block only if its outputs are finite, tau is finite and
+ *     |rho| <= tau;
+ *   - the membership check compares logits exactly in FP32 and sums split-argument FP32
+ *     softmax terms in FP64.
+ */
+#ifndef PCK_HIP_H
+#define PCK_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------------------------------------
+ * GEMV y = W x: W (m, n) row-major, x (n,) BF16, y (m,) FP32.  1 <= threads <= 1024, a power of
+ * two (>= 32 for the coalesced kernels).  Vector (16-byte) loads are used when n is a multiple of
+ * the vector width and W and x are 16-byte aligned; otherwise element loads with identical bits.
+ * -------------------------------------------------------------------------------------------*/
+
+/* BF16 weights, naive tree (contiguous chunk per lane, then neighbour pairs).
+ * Replaces pck::gemv_bf16_naive, reference src/pck/cuda/csrc/gemv_kernel.cu:204-211. */
+int pck_gemv_bf16_naive(const void* W, const void* x, float* y, int64_t m, int64_t n, int threads,
+                        void* stream);
+
+/* BF16 weights, coalesced tree with 8-column vectors.
+ * Replaces pck::gemv_bf16_coalesced, reference src/pck/cuda/csrc/gemv_kernel.cu:182-191. */
+int pck_gemv_bf16_coalesced(const void* W, const void* x, float* y, int64_t m, int64_t n,
+                            int threads, void* stream);
+
+/* OCP FP8 E4M3FN weights (unscaled codes), coalesced tree with 16-column vectors: z = Q x.
+ * Replaces pck::gemv_fp8_coalesced, reference src/pck/cuda/csrc/gemv_kernel.cu:193-202. */
+int pck_gemv_fp8_coalesced(const void* Q, const void* x, float* z, int64_t m, int64_t n,
+                           int threads, void* stream);
+
+#define PCK_MAX_GROUP 8
+
+typedef struct PckGemv {
+  const void* W; /* (m, n) BF16 or E4M3FN */
+  const void* x; /* (n,) BF16 */
+  float* y;      /* (m,) FP32 */
+  int64_t m;
+  int64_t n;
+} PckGemv;
+
+/* Up to PCK_MAX_GROUP independent GEMVs of one weight type in one launch (e.g. q, k and v of a
+ * decode layer, which share x).  Each output has exactly the bits of its single-GEMV call.
+ * weight_kind: 0 = BF16 (coalesced tree), 1 = FP8 E4M3FN.  No reference counterpart: the
+ * reference fuses such GEMVs by concatenating weights (harness/bench_decode_layer.py:48-53);
+ * a grouped launch gives the same one-launch cost without the copy. */
+int pck_gemv_group(int weight_kind, const PckGemv* gemvs, int count, int threads, void* stream);
+
+/* Launch-shape knob of the coalesced kernels, for tuning sweeps: rows per wave slot (1 or 2) and
+ * vector positions loaded ahead per lane; 0, 0 restores the built-in choice.  Changes only
+ * speed: outputs keep the same bits for every shape.  Not thread-safe; no reference
+ * counterpart. */
+int pck_gemv_set_shape(int rows_per_wave, int unroll);
+
+/* ---------------------------------------------------------------------------------------------
+ * Blocked checksum checker.  Field for field the reference's CheckDesc / CheckBatch
+ * (src/pck/cuda/csrc/checker.h:13-44); replaces pck::blocked_check
+ * (src/pck/cuda/csrc/checker_kernel.cu:189-196).
+ * -------------------------------------------------------------------------------------------*/
+
+#define PCK_MAX_BATCH 8
+
+typedef struct PckCheckDesc {
+  const float* c;          /* (K, nb, n) FP32 checksums r^T W_beta                    */
+  const void* a;           /* (nb, n) BF16 column sums of |W| per block, rounded up   */
+  const int8_t* r;         /* (K, nb, b) secret signs in {-1, +1}                     */
+  const void* x;           /* (n,) BF16                                               */
+  const float* y;          /* (nb * b,) FP32 output under check                       */
+  double* partial_cx;      /* (K, nb, segments) scratch                               */
+  double* partial_s;       /* (K, nb, segments) scratch                               */
+  unsigned int* counters;  /* (K, nb) zero on entry; left zero on exit                */
+  uint8_t* passed;         /* (K, nb) outputs: bool, rho, tau                         */
+  double* rho;
+  double* tau;
+  int64_t n;
+  int64_t seg_len;         /* ceil(n / segments)                                      */
+  int32_t block;
+  int32_t num_blocks;
+  int32_t checks;
+  int32_t segments;
+  double coef;             /* >= gamma_h + u32, rounded up                            */
+  double geps;             /* >= gamma_H(u64) + gamma_2L(u32)^2 + their product       */
+  double tau_floor;        /* >= n 2^-148                                             */
+} PckCheckDesc;
+
+typedef struct PckCheckBatch {
+  PckCheckDesc desc[PCK_MAX_BATCH];
+  int64_t start[PCK_MAX_BATCH + 1]; /* work item i belongs to check g if start[g] <= i < start[g+1] */
+  int32_t count;                    /* 1 .. PCK_MAX_BATCH */
+} PckCheckBatch;
+
+/* One launch checks every described output (K * nb * segments work items per check). */
+int pck_blocked_check(const PckCheckBatch* batch, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Sampled-token membership check for a batch of rows (top-k / top-p / greedy), the native
+ * kernel behind pck.member.check_members (reference src/pck/member.py:118-197).
+ *   logits (rows, vocab) FP32; tokens (rows,) int64 (any value: out-of-range ids reject);
+ *   top_k (rows,) int64 or NULL (already clamped to [1, vocab]; vocab = no top-k);
+ *   top_p (rows,) FP64 or NULL (1 = no top-p); greedy (rows,) uint8 or NULL;
+ *   slack = next_up(tol + member_eps32(vocab)) from the host;
+ *   k_lim = largest host-side top-k below vocab (0 if none); all_k = every host top-k < vocab;
+ *   outputs ok (rows,) uint8, above (rows,) int64, mass_above (rows,) FP64.
+ * -------------------------------------------------------------------------------------------*/
+int pck_check_members(const float* logits, int64_t rows, int64_t vocab, const int64_t* tokens,
+                      const int64_t* top_k, const double* top_p, const uint8_t* greedy,
+                      double slack, int64_t k_lim, int all_k, uint8_t* ok, int64_t* above,
+                      double* mass_above, void* stream);
+
+/* Measurement: reads `bytes` (a multiple of 16, 16-byte aligned) from `src` with `groups`
+ * workgroups of 256 lanes and stores one word per workgroup into sink[groups].  The practical
+ * HBM read ceiling for the GEMV roofline; no reference counterpart (the reference measures a
+ * device-to-device copy, src/pck/cuda/timing.py:50-55). */
+int pck_read_stream(const void* src, int64_t bytes, uint32_t* sink, int groups, void* stream);
+
+/* Text for a value returned by any entry point. */
+const char* pck_error_string(int err);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PCK_HIP_H */

@@ -1,0 +1,406 @@
+// GEMV y = W x for the decode hot path on gfx950: BF16 or OCP FP8 E4M3FN weights, BF16 x,
+// FP32 accumulation and output.
+//
+// Numerics are defined by the summation tree, not by the hardware mapping.  The coalesced tree
+// of `threads` = T virtual lanes (reference src/pck/cuda/csrc/gemv_kernel.cu:139-178, model
+// src/pck/gemv.py:71-101): virtual lane t owns the 16-byte vectors t, t + T, t + 2T, ... of a
+// row (8 BF16 or 16 FP8 columns each) and adds their products one at a time in column order,
+// starting from its first product, with columns past n contributing +0; each virtual warp of
+// 32 lanes is reduced by halving, then the T / 32 warp sums are reduced by halving.
+//
+// Hardware mapping (MI355X, wave64): one wave computes one row (two rows when T = 32).  Lane l
+// of the wave runs the T / 64 chains l, l + 64, l + 128, ... so that for every vector index the
+// wave reads 64 consecutive 16-byte vectors (1 KiB, fully coalesced), and all of a lane's loads
+// for U vector positions are issued before any product is consumed, which keeps enough bytes in
+// flight per CU to stream HBM.  The two halves of a wave are the two virtual warps 2j and
+// 2j + 1 of chain slot j, so the in-warp halving is a width-32 xor butterfly (lane 0 of each
+// half ends with exactly the halving order's value), and the warp sums are combined in the
+// halving order from uniform registers.  No LDS and no barrier are needed.
+//
+// Products: BF16 x BF16 (8 + 8 significand bits) and E4M3 x BF16 (4 + 8) are exact in FP32
+// except under underflow; they are formed with a separate v_mul_f32 and added with v_add_f32 (the
+// library is built with -ffp-contract=off), exactly the reference's __fmul_rn / __fadd_rn.  The
+// chain accumulator starts at -0.0, the additive identity of IEEE round-to-nearest, so
+// "-0 + p0" equals "start from p0" bit for bit, signed zero included.
+//
+// The naive kernel (reference gemv_kernel.cu:27-55, model src/pck/gemv.py:14-57) keeps the
+// reference's shape: one workgroup per row, a contiguous chunk per lane, an LDS pair tree.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "pck_hip.h"
+
+namespace pck {
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kWarp = 32;
+constexpr int kWavesPerGroup = 4;
+constexpr int kGroupThreads = kWave * kWavesPerGroup;
+
+struct GemvItem {
+  const void* W;
+  const uint16_t* x;
+  float* y;
+  int64_t m;
+  int64_t n;
+  int64_t per_lane;  // vectors per virtual lane: ceil(ceil(n / vec) / T)
+};
+
+struct GemvBatch {
+  GemvItem item[PCK_MAX_GROUP];
+  int64_t first_group[PCK_MAX_GROUP + 1];  // workgroup prefix sums
+  int count;
+};
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// Two E4M3FN codes (bytes 0-1, or 2-3 with kHigh) of `w` to FP32, exactly (hardware OCP decode).
+template <bool kHigh>
+__device__ __forceinline__ float2 fp8_pair(uint32_t w) {
+  auto v = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), kHigh);
+  return make_float2(v[0], v[1]);
+}
+
+__device__ __forceinline__ float fp8_one(uint8_t code) { return fp8_pair<false>(code).x; }
+
+// Adds the products of one vector to `acc`, in column order.
+template <bool kFp8>
+__device__ __forceinline__ void add_products(float& acc, const uint4& w, const uint4& xa,
+                                             const uint4& xb) {
+  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+  if constexpr (!kFp8) {
+    const uint32_t xd[4] = {xa.x, xa.y, xa.z, xa.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float p0 = bf16_lo(wd[k]) * bf16_lo(xd[k]);
+      const float p1 = bf16_hi(wd[k]) * bf16_hi(xd[k]);
+      acc = acc + p0;
+      acc = acc + p1;
+    }
+  } else {
+    const uint32_t xd[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float2 f01 = fp8_pair<false>(wd[k]);
+      const float2 f23 = fp8_pair<true>(wd[k]);
+      const float p0 = f01.x * bf16_lo(xd[2 * k]);
+      const float p1 = f01.y * bf16_hi(xd[2 * k]);
+      const float p2 = f23.x * bf16_lo(xd[2 * k + 1]);
+      const float p3 = f23.y * bf16_hi(xd[2 * k + 1]);
+      acc = acc + p0;
+      acc = acc + p1;
+      acc = acc + p2;
+      acc = acc + p3;
+    }
+  }
+}
+
+// Element loads for rows that cannot take 16-byte vectors (n not a multiple of the vector width
+// or a misaligned pointer): the same products in the same order, +0 past n.
+template <bool kFp8>
+__device__ __forceinline__ void add_products_scalar(float& acc, const void* w_row,
+                                                    const uint16_t* x, int64_t col, int64_t n) {
+  constexpr int V = kFp8 ? 16 : 8;
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    const int64_t j = col + k;
+    float p = 0.0f;
+    if (j < n) {
+      const float xv = __uint_as_float(static_cast<uint32_t>(x[j]) << 16);
+      float wv;
+      if constexpr (kFp8) {
+        wv = fp8_one(static_cast<const uint8_t*>(w_row)[j]);
+      } else {
+        wv = __uint_as_float(static_cast<uint32_t>(static_cast<const uint16_t*>(w_row)[j]) << 16);
+      }
+      p = wv * xv;
+    }
+    acc = acc + p;
+  }
+}
+
+__device__ __forceinline__ float xor32(float v, int offset) { return __shfl_xor(v, offset, kWarp); }
+
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// T virtual lanes per row, R rows per wave slot, U vector positions loaded ahead.
+// kPad: some vectors of a chain lie past n (n is not a multiple of T * vec), so loads of those
+// are redirected to column 0 and their data replaced by zeros.  kVector: 16-byte loads (n is a
+// multiple of vec and the pointers are aligned); otherwise element loads.
+template <int T, int R, int U, bool kFp8, bool kVector, bool kPad>
+__global__ void __launch_bounds__(kGroupThreads) gemv_tree_kernel(const GemvBatch batch) {
+  constexpr int V = kFp8 ? 16 : 8;
+  constexpr int kLanesPerRow = T >= kWave ? kWave : T;
+  constexpr int kSlots = kWave / kLanesPerRow;  // rows side by side in one wave (2 if T = 32)
+  constexpr int kChains = T / kLanesPerRow;     // chains per lane
+  constexpr int kElemBytes = kFp8 ? 1 : 2;
+
+  int g = 0;
+  while (g + 1 < batch.count && static_cast<int64_t>(blockIdx.x) >= batch.first_group[g + 1]) ++g;
+  const GemvItem& it = batch.item[g];
+  const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
+  const int64_t wave =
+      (static_cast<int64_t>(blockIdx.x) - batch.first_group[g]) * kWavesPerGroup +
+      (static_cast<int>(threadIdx.x) >> 6);
+  const int slot = lane / kLanesPerRow;
+  const int chain0 = lane % kLanesPerRow;
+  const int64_t n = it.n;
+  const int64_t P = it.per_lane;
+  const uint16_t* __restrict__ x = it.x;
+
+  // Rows past m compute on row m - 1 (a valid address) and are not stored.
+  const unsigned char* w_rows[R];
+  bool live[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t row = (wave * kSlots + slot) * R + r;
+    live[r] = row < it.m;
+    w_rows[r] =
+        static_cast<const unsigned char*>(it.W) + (live[r] ? row : it.m - 1) * n * kElemBytes;
+  }
+
+  float acc[R][kChains];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < kChains; ++j) acc[r][j] = -0.0f;
+
+  for (int64_t v0 = 0; v0 < P; v0 += U) {
+    if constexpr (kVector) {
+      uint4 wb[U][R][kChains];
+      uint4 xa[U][kChains];
+      uint4 xb[U][kChains];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (U > 1 && v0 + u >= P) break;  // uniform: the tail of the last block
+#pragma unroll
+        for (int j = 0; j < kChains; ++j) {
+          const int64_t col = ((v0 + u) * T + chain0 + kLanesPerRow * j) * V;
+          const int64_t at = (!kPad || col < n) ? col : 0;
+          xa[u][j] = *reinterpret_cast<const uint4*>(x + at);
+          if constexpr (kFp8) xb[u][j] = *reinterpret_cast<const uint4*>(x + at + 8);
+#pragma unroll
+          for (int r = 0; r < R; ++r)
+            wb[u][r][j] = *reinterpret_cast<const uint4*>(w_rows[r] + at * kElemBytes);
+          if constexpr (kPad) {
+            if (col >= n) {  // a padding vector: +0 products (0 x 0)
+              xa[u][j] = make_uint4(0, 0, 0, 0);
+              xb[u][j] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+              for (int r = 0; r < R; ++r) wb[u][r][j] = make_uint4(0, 0, 0, 0);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (U > 1 && v0 + u >= P) break;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int j = 0; j < kChains; ++j)
+            add_products<kFp8>(acc[r][j], wb[u][r][j], xa[u][j], kFp8 ? xb[u][j] : xa[u][j]);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int j = 0; j < kChains; ++j) {
+          const int64_t col = (v0 * T + chain0 + kLanesPerRow * j) * V;
+          add_products_scalar<kFp8>(acc[r][j], w_rows[r], x, col, n);
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    // Halving inside each 32-lane virtual warp (width-32 xor butterfly: lane 0 of each half
+    // holds a[0] after a[i] += a[i + 16], a[i] += a[i + 8], ..., a[0] += a[1]).
+#pragma unroll
+    for (int j = 0; j < kChains; ++j) {
+#pragma unroll
+      for (int off = kWarp / 2; off > 0; off /= 2) acc[r][j] = acc[r][j] + xor32(acc[r][j], off);
+    }
+    const int64_t row = (wave * kSlots + slot) * R + r;
+    if constexpr (kSlots == 2) {
+      // T = 32: one virtual warp per row; lanes 0 and 32 hold the two rows' sums.
+      if (chain0 == 0 && live[r]) it.y[row] = acc[r][0];
+    } else {
+      // Warp w = 2j + h is half h of chain slot j; reduce the T / 32 warp sums by halving.
+      constexpr int kWarps = 2 * kChains;
+      float ws[kWarps];
+#pragma unroll
+      for (int j = 0; j < kChains; ++j) {
+        ws[2 * j] = lane_value(acc[r][j], 0);
+        ws[2 * j + 1] = lane_value(acc[r][j], kWarp);
+      }
+#pragma unroll
+      for (int half = kWarps / 2; half > 0; half /= 2)
+#pragma unroll
+        for (int i = 0; i < half; ++i) ws[i] = ws[i] + ws[i + half];
+      if (lane == 0 && live[r]) it.y[row] = ws[0];
+    }
+  }
+}
+
+// Naive tree: one workgroup of `threads` lanes per row (reference gemv_kernel.cu:27-55).
+__global__ void __launch_bounds__(1024)
+    gemv_naive_kernel(const uint16_t* __restrict__ W, const uint16_t* __restrict__ x,
+                      float* __restrict__ y, int64_t n, int64_t chunk) {
+  extern __shared__ float partial[];
+  const int t = static_cast<int>(threadIdx.x);
+  const uint16_t* w_row = W + static_cast<int64_t>(blockIdx.x) * n;
+  const int64_t begin = t * chunk;
+  auto product = [&](int64_t j) {
+    const float wv = __uint_as_float(static_cast<uint32_t>(w_row[j]) << 16);
+    const float xv = __uint_as_float(static_cast<uint32_t>(x[j]) << 16);
+    return wv * xv;
+  };
+  float acc = begin < n ? product(begin) : 0.0f;
+  for (int64_t j = begin + 1; j < begin + chunk; ++j) acc = acc + (j < n ? product(j) : 0.0f);
+  partial[t] = acc;
+  __syncthreads();
+  for (int stride = 1; stride < static_cast<int>(blockDim.x); stride *= 2) {
+    if (t % (2 * stride) == 0) partial[t] = partial[t] + partial[t + stride];
+    __syncthreads();
+  }
+  if (t == 0) y[blockIdx.x] = partial[0];
+}
+
+// Launch shape of the coalesced kernel: rows per wave slot and vector positions loaded ahead.
+struct TreeShape {
+  int rows;
+  int unroll;
+};
+
+TreeShape g_shape_override = {0, 0};
+
+TreeShape choose_shape(int threads, int64_t per_lane) {
+  if (g_shape_override.rows > 0) return g_shape_override;
+  (void)threads;
+  return TreeShape{1, per_lane >= 4 ? 4 : 2};
+}
+
+template <int T, int R, int U, bool kFp8, bool kVector, bool kPad>
+hipError_t launch_tree(GemvBatch& batch, hipStream_t stream) {
+  constexpr int kLanesPerRow = T >= kWave ? kWave : T;
+  constexpr int64_t kRowsPerGroup = (kWave / kLanesPerRow) * R * kWavesPerGroup;
+  batch.first_group[0] = 0;
+  for (int g = 0; g < batch.count; ++g) {
+    batch.first_group[g + 1] =
+        batch.first_group[g] + (batch.item[g].m + kRowsPerGroup - 1) / kRowsPerGroup;
+  }
+  const int64_t groups = batch.first_group[batch.count];
+  if (groups == 0) return hipSuccess;
+  if (groups * kGroupThreads > 0xFFFFFFFFll) return hipErrorInvalidValue;  // 32-bit dispatch size
+  gemv_tree_kernel<T, R, U, kFp8, kVector, kPad>
+      <<<dim3(static_cast<unsigned>(groups)), dim3(kGroupThreads), 0, stream>>>(batch);
+  return hipGetLastError();
+}
+
+template <int T, bool kFp8, bool kPad>
+hipError_t launch_vector(GemvBatch& batch, TreeShape shape, hipStream_t s) {
+  if (shape.rows == 2) return launch_tree<T, 2, 2, kFp8, true, kPad>(batch, s);
+  if (shape.unroll >= 4) return launch_tree<T, 1, 4, kFp8, true, kPad>(batch, s);
+  return launch_tree<T, 1, 2, kFp8, true, kPad>(batch, s);
+}
+
+template <int T, bool kFp8>
+hipError_t launch_for_threads(GemvBatch& batch, bool vector, bool pad, TreeShape shape,
+                              hipStream_t s) {
+  if (!vector) return launch_tree<T, 1, 1, kFp8, false, true>(batch, s);
+  return pad ? launch_vector<T, kFp8, true>(batch, shape, s)
+             : launch_vector<T, kFp8, false>(batch, shape, s);
+}
+
+template <bool kFp8>
+hipError_t launch_group(const PckGemv* gemvs, int count, int threads, hipStream_t stream) {
+  constexpr int V = kFp8 ? 16 : 8;
+  if (count < 1 || count > PCK_MAX_GROUP || gemvs == nullptr) return hipErrorInvalidValue;
+  if (threads < kWarp || threads > 1024 || (threads & (threads - 1)) != 0)
+    return hipErrorInvalidValue;
+  GemvBatch batch{};
+  batch.count = count;
+  bool vector = true;
+  bool pad = false;
+  int64_t max_per_lane = 1;
+  for (int g = 0; g < count; ++g) {
+    const PckGemv& d = gemvs[g];
+    if (d.m < 0 || d.m > 0x7FFFFFFF || (d.m > 0 && (d.n < 1 || !d.W || !d.x || !d.y)))
+      return hipErrorInvalidValue;
+    const int64_t n = d.m > 0 ? d.n : 1;
+    const int64_t per_lane = ((n + V - 1) / V + threads - 1) / threads;
+    batch.item[g] = GemvItem{d.W, static_cast<const uint16_t*>(d.x), d.y, d.m, n, per_lane};
+    if (d.m > 0) {
+      vector = vector && n % V == 0 && reinterpret_cast<uintptr_t>(d.W) % 16 == 0 &&
+               reinterpret_cast<uintptr_t>(d.x) % 16 == 0;
+      max_per_lane = per_lane > max_per_lane ? per_lane : max_per_lane;
+      pad = pad || n % (static_cast<int64_t>(threads) * V) != 0;
+    }
+  }
+  const TreeShape shape = choose_shape(threads, max_per_lane);
+  switch (threads) {
+    case 32: return launch_for_threads<32, kFp8>(batch, vector, pad, shape, stream);
+    case 64: return launch_for_threads<64, kFp8>(batch, vector, pad, shape, stream);
+    case 128: return launch_for_threads<128, kFp8>(batch, vector, pad, shape, stream);
+    case 256: return launch_for_threads<256, kFp8>(batch, vector, pad, shape, stream);
+    case 512: return launch_for_threads<512, kFp8>(batch, vector, pad, shape, stream);
+    default: return launch_for_threads<1024, kFp8>(batch, vector, pad, shape, stream);
+  }
+}
+
+}  // namespace
+}  // namespace pck
+
+extern "C" {
+
+int pck_gemv_bf16_coalesced(const void* W, const void* x, float* y, int64_t m, int64_t n,
+                            int threads, void* stream) {
+  const PckGemv one{W, x, y, m, n};
+  return pck::launch_group<false>(&one, 1, threads, static_cast<hipStream_t>(stream));
+}
+
+int pck_gemv_fp8_coalesced(const void* Q, const void* x, float* z, int64_t m, int64_t n,
+                           int threads, void* stream) {
+  const PckGemv one{Q, x, z, m, n};
+  return pck::launch_group<true>(&one, 1, threads, static_cast<hipStream_t>(stream));
+}
+
+int pck_gemv_group(int weight_kind, const PckGemv* gemvs, int count, int threads, void* stream) {
+  if (weight_kind == 0)
+    return pck::launch_group<false>(gemvs, count, threads, static_cast<hipStream_t>(stream));
+  if (weight_kind == 1)
+    return pck::launch_group<true>(gemvs, count, threads, static_cast<hipStream_t>(stream));
+  return hipErrorInvalidValue;
+}
+
+int pck_gemv_bf16_naive(const void* W, const void* x, float* y, int64_t m, int64_t n, int threads,
+                        void* stream) {
+  if (threads < 1 || threads > 1024 || (threads & (threads - 1)) != 0) return hipErrorInvalidValue;
+  if (m < 0 || m > 0x7FFFFFFF || m * threads > 0xFFFFFFFFll) return hipErrorInvalidValue;
+  if (m == 0) return hipSuccess;
+  if (n < 1 || !W || !x || !y) return hipErrorInvalidValue;
+  const int64_t chunk = (n + threads - 1) / threads;
+  pck::gemv_naive_kernel<<<dim3(static_cast<unsigned>(m)), dim3(threads),
+                           static_cast<size_t>(threads) * sizeof(float),
+                           static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(W), static_cast<const uint16_t*>(x), y, n, chunk);
+  return hipGetLastError();
+}
+
+int pck_gemv_set_shape(int rows_per_wave, int unroll) {
+  if (rows_per_wave < 0 || rows_per_wave > 2 || unroll < 0) return hipErrorInvalidValue;
+  pck::g_shape_override = pck::TreeShape{rows_per_wave, unroll};
+  return hipSuccess;
+}
+
+const char* pck_error_string(int err) { return hipGetErrorString(static_cast<hipError_t>(err)); }
+
+}  // extern "C"

@@ -1,0 +1,81 @@
+"""Builds libpck_hip.so, the gfx950 HIP library behind `pck.cuda` and `pck.member`.
+
+Run ``python -m pck._build`` (with ``proof-carrying-kernels_amd`` on ``sys.path``) or call
+`build`.  hipcc cross-compiles for gfx950 without a GPU.  The library lands next to this file
+so it travels with the source tree; it is never installed into site-packages.
+
+Flags that the numerics depend on:
+  -ffp-contract=off   no mul + add -> FMA contraction (the GEMV adds rounded products, and the
+                      checker's error-free transformations need separate roundings);
+  no -ffast-math and no denormal flushing (kernel descriptors keep FP32/FP64 denormals);
+  -target-feature -packed-fp32-ops   no packed FP32 instructions in any kernel.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PACKAGE = Path(__file__).resolve().parent
+ROOT = PACKAGE.parent
+CSRC = ROOT / "csrc"
+INCLUDE = ROOT.parent / "include"
+LIBRARY = PACKAGE / "libpck_hip.so"
+SOURCES = ("gemv.hip", "checker.hip", "member.hip", "measure.hip")
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-mcode-object-version=5",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-ffp-contract=off",
+    "-fno-fast-math",
+    "-Wall",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+]
+
+
+def hipcc() -> str:
+    found = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(found).exists():
+        raise RuntimeError("hipcc not found (ROCm is required to build libpck_hip.so)")
+    return found
+
+
+def _compile(src: Path, obj: Path) -> None:
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stderr}")
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every source in csrc/ and link libpck_hip.so; returns its path."""
+    out_dir = ROOT / "_build"
+    out_dir.mkdir(exist_ok=True)
+    sources = [CSRC / s for s in SOURCES if (CSRC / s).exists()]
+    objects = [out_dir / (s.stem + ".o") for s in sources]
+    jobs = min(len(sources), max(1, int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with ThreadPoolExecutor(jobs) as pool:
+        list(pool.map(_compile, sources, objects))
+    tmp = LIBRARY.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"linking libpck_hip.so failed:\n{res.stderr}")
+    os.replace(tmp, LIBRARY)
+    if verbose:
+        print(f"built {LIBRARY}")
+    return LIBRARY
+
+
+if __name__ == "__main__":
+    build(verbose=True)

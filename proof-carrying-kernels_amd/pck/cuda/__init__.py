@@ -1,0 +1,29 @@
+"""GPU entry points of the decode hot path (reference `src/pck/cuda/__init__.py`), backed by
+the gfx950 library libpck_hip.so.  ``pck.cuda`` keeps the reference's module name: on ROCm,
+PyTorch's device API is ``torch.cuda``."""
+
+from pck.cuda.checker import (
+    DEFAULT_BLOCK,
+    CheckResult,
+    GpuBlockedChecker,
+    PendingCheck,
+    SideStreamChecker,
+    check_many,
+    round_up_bf16,
+)
+from pck.cuda.gemv import gemv_coalesced, gemv_fp8, gemv_group, gemv_naive, quantize_fp8
+
+__all__ = [
+    "DEFAULT_BLOCK",
+    "CheckResult",
+    "GpuBlockedChecker",
+    "PendingCheck",
+    "SideStreamChecker",
+    "check_many",
+    "gemv_coalesced",
+    "gemv_fp8",
+    "gemv_group",
+    "gemv_naive",
+    "quantize_fp8",
+    "round_up_bf16",
+]

@@ -1,0 +1,329 @@
+"""Trusted blocked checksum checker on the GPU (reference `src/pck/cuda/checker.py`).
+
+The checksum bank (secret signs r, FP32 checksums c = r^T W_beta, and a_beta = sum |W_i|
+rounded up to BF16) is built once at weight load.  In production the fault model is
+non-adversarial, so signs drawn ahead of time are fine; an adversarial evaluation must draw
+them after the untrusted kernel has finished.  The check itself is one launch of the HIP
+kernel `pck_blocked_check` for up to eight GEMV outputs.
+"""
+
+from __future__ import annotations
+
+import math
+from collections.abc import Sequence
+from dataclasses import dataclass
+
+import torch
+
+from pck.cuda._lib import MAX_BATCH, PckCheckBatch, PckCheckDesc, check, lib, stream_handle
+from pck.fp import U32, U64, ceil_div, gamma, next_up, sum_up_factor
+
+DEFAULT_BLOCK = 128
+"""Rows per checksum (reference `src/pck/cuda/checker.py:20-22`)."""
+
+KERNEL_THREADS = 256  # lanes per workgroup of the checker kernel
+BLOCKS_PER_SM = 4  # workgroups per CU the default segment count aims for
+MIN_SEGMENT_COLUMNS = 2 * KERNEL_THREADS
+
+_DTYPE_NAMES = {
+    torch.float32: "Float",
+    torch.float64: "Double",
+    torch.bfloat16: "BFloat16",
+    torch.int8: "Char",
+    torch.int32: "Int",
+    torch.int64: "Long",
+    torch.uint8: "Byte",
+    torch.bool: "Bool",
+    torch.float16: "Half",
+}
+
+
+def _dtype_name(dtype: torch.dtype) -> str:
+    return _DTYPE_NAMES.get(dtype, str(dtype).removeprefix("torch."))
+
+
+def round_up_bf16(v: torch.Tensor) -> torch.Tensor:
+    """Non-negative FP64 values to BF16, never rounded down (reference
+    `src/pck/cuda/checker.py:29-43`): up to FP32 first, then up to BF16 by carrying into the
+    top 16 bits whenever a low bit is set.  Values past the BF16 range become +Inf."""
+    if v.dtype != torch.float64:
+        raise TypeError(f"round_up_bf16 expects float64, got {v.dtype}")
+    if bool((v < 0).any()):
+        raise ValueError("round_up_bf16 expects non-negative values")
+    f = v.float()
+    f = torch.where(f.double() < v, torch.nextafter(f, torch.full_like(f, math.inf)), f)
+    bits = f.view(torch.int32)
+    bits = torch.where((bits & 0xFFFF) != 0, (bits + 0x10000) & -0x10000, bits)
+    return bits.view(torch.float32).to(torch.bfloat16)  # exact: the low 16 bits are zero
+
+
+@dataclass(frozen=True)
+class CheckResult:
+    """Per (check, block) outcome; each tensor has shape (checks, num_blocks)."""
+
+    passed: torch.Tensor
+    rho: torch.Tensor
+    tau: torch.Tensor
+
+    @property
+    def verdict(self) -> torch.Tensor:
+        """Per-block verdict: True only if the block passed every check."""
+        return self.passed.all(dim=0)
+
+
+class GpuBlockedChecker:
+    """Checks y = W x one block of ``block`` rows at a time, with ``checks`` sign draws
+    (reference `src/pck/cuda/checker.py:60-137`).
+
+    ``height`` is the summation-tree height of the GEMV being checked (e.g.
+    ``tree_height(n, threads, vec)``).  ``segments`` splits each block's n columns over that
+    many workgroups (default about ``BLOCKS_PER_SM`` per CU).  A checker owns its scratch, so
+    use it from one stream at a time.
+    """
+
+    def __init__(
+        self,
+        W: torch.Tensor,
+        block: int,
+        height: int,
+        checks: int = 1,
+        generator: torch.Generator | None = None,
+        segments: int | None = None,
+    ) -> None:
+        if not (W.is_cuda and W.dtype == torch.bfloat16 and W.dim() == 2):
+            raise ValueError("W must be a 2-D bfloat16 CUDA tensor")
+        m, n = W.shape
+        if block < 1 or m % block:
+            raise ValueError(f"block={block} must be positive and divide m={m}")
+        if checks < 1:
+            raise ValueError(f"checks must be positive, got {checks}")
+        self.m, self.n, self.block, self.checks = m, n, block, checks
+        self.num_blocks = m // block
+
+        # Signs from a CPU generator, as the reference draws them (the same generator state
+        # gives the same signs).
+        bits = torch.randint(0, 2, (checks, self.num_blocks, block), generator=generator)
+        self.r = (2 * bits - 1).to(torch.int8).to(W.device)
+
+        W64 = W.view(self.num_blocks, block, n).double()
+        c = torch.empty((checks, self.num_blocks, n), dtype=torch.float32, device=W.device)
+        for k in range(checks):  # one draw at a time bounds the FP64 temporaries
+            c[k] = torch.einsum("bi,bin->bn", self.r[k].double(), W64).float()
+        self.c = c
+
+        # The FP64 column sum rounds to nearest: lift it to an upper bound, then round up.
+        col = W64.abs().sum(dim=1) * sum_up_factor(block)
+        self.a = round_up_bf16(torch.nextafter(col, torch.full_like(col, math.inf)))
+        del W64
+        if not bool(torch.isfinite(self.a).all()):
+            raise ValueError("sum of |W| over a block overflows BF16")
+
+        self.coef = next_up(gamma(height) + U32, 2)
+        if segments is None:
+            cus = torch.cuda.get_device_properties(W.device).multi_processor_count
+            wanted = ceil_div(BLOCKS_PER_SM * cus, checks * self.num_blocks)
+            segments = max(1, min(wanted, n // MIN_SEGMENT_COLUMNS))
+        if not 1 <= segments <= min(n, 65535):
+            raise ValueError(f"segments must be in [1, {min(n, 65535)}], got {segments}")
+        self.segments = segments
+        # geps keeps the reference's form: the FP32 Dot2 chain term of its kernel
+        # (gamma_2L(u32)^2, L terms per chain) and the FP64 height H of rho's evaluation,
+        # compounded.  The HIP kernel evaluates rho in FP64 with exact products, whose error
+        # gamma_H(u64) (sum |c_j x_j| + sum |y|) is within the gH term alone.
+        chain = ceil_div(ceil_div(n, segments), KERNEL_THREADS)
+        g2 = gamma(2 * chain, U32) ** 2
+        fp64_height = max(n + block + 1, 21 + segments + ceil_div(block, KERNEL_THREADS))
+        gh = gamma(fp64_height, U64)
+        self.geps = next_up(gh + g2 + gh * g2, 4)
+        self.tau_floor = next_up(n * 2.0**-148, 2)
+        scratch = (checks, self.num_blocks, segments)
+        self._partial_cx = torch.empty(scratch, dtype=torch.float64, device=W.device)
+        self._partial_s = torch.empty(scratch, dtype=torch.float64, device=W.device)
+        self._counters = torch.zeros((checks, self.num_blocks), dtype=torch.int32, device=W.device)
+
+    def check(self, x: torch.Tensor, y: torch.Tensor) -> CheckResult:
+        """Run every check on output ``y`` of the GEMV for input ``x``."""
+        return check_many([(self, x, y)])[0]
+
+    def verdict(self, x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+        """Per-block pass/fail (True = passed every check)."""
+        return self.check(x, y).verdict
+
+
+MAX_BATCH_CHECKS = MAX_BATCH
+
+
+def _check_tensor(t: torch.Tensor, name: str, dtype: torch.dtype, device: torch.device) -> None:
+    if not (t.is_cuda and t.device == device):
+        raise RuntimeError(f"{name} must be on {device}")
+    if t.dtype != dtype:
+        raise RuntimeError(f"{name} must be {_dtype_name(dtype)}, got {_dtype_name(t.dtype)}")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+
+
+def _describe(
+    c: torch.Tensor, a: torch.Tensor, r: torch.Tensor, x: torch.Tensor, y: torch.Tensor,
+    partial_cx: torch.Tensor, partial_s: torch.Tensor, counters: torch.Tensor, coef: float,
+    geps: float, tau_floor: float, device: torch.device,
+) -> tuple[PckCheckDesc, tuple[torch.Tensor, torch.Tensor, torch.Tensor]]:  # fmt: skip
+    """Validates one check (reference `bindings.cpp:164-218`, same order and text) and
+    returns its descriptor and freshly allocated outputs (passed, rho, tau)."""
+    _check_tensor(c, "c", torch.float32, device)
+    _check_tensor(a, "a", torch.bfloat16, device)
+    _check_tensor(r, "r", torch.int8, device)
+    _check_tensor(x, "x", torch.bfloat16, device)
+    _check_tensor(y, "y", torch.float32, device)
+    _check_tensor(partial_cx, "partial_cx", torch.float64, device)
+    _check_tensor(partial_s, "partial_s", torch.float64, device)
+    _check_tensor(counters, "counters", torch.int32, device)
+    if not (c.dim() == 3 and a.dim() == 2 and r.dim() == 3 and x.dim() == 1 and y.dim() == 1):
+        raise RuntimeError("expected c (K, nb, n), a (nb, n), r (K, nb, b), x (n,), y (m,)")
+    checks, num_blocks, n = c.shape
+    block = r.size(2)
+    if not (a.size(0) == num_blocks and a.size(1) == n):
+        raise RuntimeError("a must have shape (nb, n)")
+    if not (r.size(0) == checks and r.size(1) == num_blocks):
+        raise RuntimeError("r must have shape (K, nb, b)")
+    if x.size(0) != n:
+        raise RuntimeError("x must have shape (n,)")
+    if y.size(0) != num_blocks * block:
+        raise RuntimeError("y must have shape (nb * b,)")
+    if not (checks >= 1 and num_blocks >= 1 and n >= 1 and block >= 1):
+        raise RuntimeError("empty checker")
+    if not (
+        partial_cx.dim() == 3
+        and partial_cx.size(0) == checks
+        and partial_cx.size(1) == num_blocks
+        and partial_s.shape == partial_cx.shape
+    ):
+        raise RuntimeError("partial sums must have shape (K, nb, segments)")
+    if not (counters.dim() == 2 and counters.size(0) == checks and counters.size(1) == num_blocks):
+        raise RuntimeError("counters must have shape (K, nb)")
+    segments = partial_cx.size(2)
+    if not 1 <= segments <= n:
+        raise RuntimeError(f"segments must be in [1, n], got {segments}")
+    if not (coef > 0 and geps > 0 and tau_floor > 0):
+        raise RuntimeError("coef, geps and floor must be positive")
+    shape = (checks, num_blocks)
+    passed = torch.empty(shape, dtype=torch.bool, device=device)
+    rho = torch.empty(shape, dtype=torch.float64, device=device)
+    tau = torch.empty(shape, dtype=torch.float64, device=device)
+    desc = PckCheckDesc(
+        c.data_ptr(), a.data_ptr(), r.data_ptr(), x.data_ptr(), y.data_ptr(),
+        partial_cx.data_ptr(), partial_s.data_ptr(), counters.data_ptr(), passed.data_ptr(),
+        rho.data_ptr(), tau.data_ptr(), n, ceil_div(n, segments), block, num_blocks, checks,
+        segments, coef, geps, tau_floor,
+    )  # fmt: skip
+    return desc, (passed, rho, tau)
+
+
+def blocked_check(
+    c: Sequence[torch.Tensor], a: Sequence[torch.Tensor], r: Sequence[torch.Tensor],
+    x: Sequence[torch.Tensor], y: Sequence[torch.Tensor], partial_cx: Sequence[torch.Tensor],
+    partial_s: Sequence[torch.Tensor], counters: Sequence[torch.Tensor], coef: Sequence[float],
+    geps: Sequence[float], tau_floor: Sequence[float],
+) -> list[tuple[torch.Tensor, torch.Tensor, torch.Tensor]]:  # fmt: skip
+    """Checks up to eight GEMV outputs in one launch; (passed, rho, tau) per check.
+
+    The native entry of the reference's extension (`bindings.cpp:221-256`): same argument
+    lists, validation order and messages; the launch goes to `pck_blocked_check`.
+    """
+    count = len(c)
+    if not 1 <= count <= MAX_BATCH:
+        raise RuntimeError(f"batch size must be in [1, {MAX_BATCH}], got {count}")
+    lists = (a, r, x, y, partial_cx, partial_s, counters, coef, geps, tau_floor)
+    if any(len(v) != count for v in lists):
+        raise RuntimeError("all argument lists must have the same length")
+    if not y[0].is_cuda:
+        raise RuntimeError("y must be a CUDA tensor")
+    device = y[0].device
+    handle = lib()
+    batch = PckCheckBatch()
+    batch.count = count
+    outputs = []
+    for g in range(count):
+        if not y[g].is_cuda:
+            raise RuntimeError("y must be a CUDA tensor")
+        desc, out = _describe(
+            c[g], a[g], r[g], x[g], y[g], partial_cx[g], partial_s[g], counters[g], coef[g],
+            geps[g], tau_floor[g], device,
+        )  # fmt: skip
+        batch.desc[g] = desc
+        batch.start[g + 1] = batch.start[g] + desc.checks * desc.num_blocks * desc.segments
+        outputs.append(out)
+    if batch.start[count] > 2**31 - 1:
+        raise RuntimeError("too many blocks")
+    with torch.cuda.device(device):
+        err = handle.pck_blocked_check(batch, stream_handle(device))
+    check(err, "checker kernel launch")
+    return outputs
+
+
+def check_many(
+    items: Sequence[tuple[GpuBlockedChecker, torch.Tensor, torch.Tensor]],
+) -> list[CheckResult]:
+    """Check several GEMV outputs, ``(checker, x, y)`` each, eight per launch (reference
+    `src/pck/cuda/checker.py:143-171`).  Each checker may appear only once per call, since a
+    launch uses its scratch."""
+    if len({id(checker) for checker, _, _ in items}) != len(items):
+        raise ValueError("each checker may appear only once per call")
+    results: list[CheckResult] = []
+    for i in range(0, len(items), MAX_BATCH):
+        chunk = items[i : i + MAX_BATCH]
+        outputs = blocked_check(
+            [ch.c for ch, _, _ in chunk],
+            [ch.a for ch, _, _ in chunk],
+            [ch.r for ch, _, _ in chunk],
+            [x for _, x, _ in chunk],
+            [y for _, _, y in chunk],
+            [ch._partial_cx for ch, _, _ in chunk],
+            [ch._partial_s for ch, _, _ in chunk],
+            [ch._counters for ch, _, _ in chunk],
+            [ch.coef for ch, _, _ in chunk],
+            [ch.geps for ch, _, _ in chunk],
+            [ch.tau_floor for ch, _, _ in chunk],
+        )
+        results.extend(CheckResult(passed, rho, tau) for passed, rho, tau in outputs)
+    return results
+
+
+class PendingCheck:
+    """A check queued on a side stream; `wait` makes the current stream wait for it
+    (reference `src/pck/cuda/checker.py:174-186`)."""
+
+    def __init__(self, result: CheckResult, done: torch.cuda.Event) -> None:
+        self._result = result
+        self._done = done
+
+    def wait(self) -> CheckResult:
+        stream = torch.cuda.current_stream()
+        stream.wait_event(self._done)
+        for t in (self._result.passed, self._result.rho, self._result.tau):
+            t.record_stream(stream)
+        return self._result
+
+
+class SideStreamChecker:
+    """Runs checks on a dedicated stream (default priority) so they overlap later work; each
+    check waits for an event recorded on the caller's stream at submit time, so it starts only
+    after the GEMV that produced y (reference `src/pck/cuda/checker.py:189-215`)."""
+
+    def __init__(self, device: torch.device | None = None) -> None:
+        self.stream = torch.cuda.Stream(device)
+
+    def submit(self, checker: GpuBlockedChecker, x: torch.Tensor, y: torch.Tensor) -> PendingCheck:
+        ready = torch.cuda.Event()
+        ready.record(torch.cuda.current_stream())
+        with torch.cuda.stream(self.stream):
+            self.stream.wait_event(ready)
+            x.record_stream(self.stream)  # keep the allocator from reusing x and y early
+            y.record_stream(self.stream)
+            result = checker.check(x, y)
+            done = torch.cuda.Event()
+            done.record(self.stream)
+        return PendingCheck(result, done)
+
+    def wait_all(self) -> None:
+        """Make the current stream wait for every check submitted so far."""
+        torch.cuda.current_stream().wait_stream(self.stream)

@@ -1,0 +1,82 @@
+"""The C ABI of libpck_hip.so, checked without a GPU: the library loads, exports every function
+include/pck_hip.h declares, and the ctypes mirrors of its structs have the header's layout
+(gcc compiles the header and prints sizeof / offsetof)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from pck.cuda import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "pck_hip.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(pck_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_entry_points() -> None:
+    names = declared_functions()
+    for expected in (
+        "pck_gemv_bf16_naive",
+        "pck_gemv_bf16_coalesced",
+        "pck_gemv_fp8_coalesced",
+        "pck_gemv_group",
+        "pck_blocked_check",
+        "pck_check_members",
+        "pck_error_string",
+    ):
+        assert expected in names
+
+
+def test_library_exports_every_declared_function() -> None:
+    handle = _lib.lib()
+    for name in declared_functions():
+        assert hasattr(handle, name), name
+    assert set(declared_functions()) >= set(_lib.SIGNATURES)
+
+
+def test_error_strings() -> None:
+    assert _lib.lib().pck_error_string(0) == b"no error"
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        _lib.check(1, "probe")
+
+
+LAYOUT_PROGRAM = r"""
+#include <stddef.h>
+#include <stdio.h>
+#include "pck_hip.h"
+#define F(T, f) printf(#T "." #f " %zu\n", offsetof(T, f));
+int main(void) {
+  printf("PckGemv %zu\nPckCheckDesc %zu\nPckCheckBatch %zu\n", sizeof(PckGemv),
+         sizeof(PckCheckDesc), sizeof(PckCheckBatch));
+  F(PckGemv, W) F(PckGemv, m) F(PckGemv, n)
+  F(PckCheckDesc, tau) F(PckCheckDesc, n) F(PckCheckDesc, seg_len) F(PckCheckDesc, block)
+  F(PckCheckDesc, segments) F(PckCheckDesc, coef) F(PckCheckDesc, tau_floor)
+  F(PckCheckBatch, start) F(PckCheckBatch, count)
+  return 0;
+}
+"""
+
+
+def test_struct_layouts_match_the_header(tmp_path: Path) -> None:
+    src = tmp_path / "layout.c"
+    src.write_text(LAYOUT_PROGRAM)
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", f"-I{HEADER.parent}", str(src), "-o", str(exe)], check=True)
+    lines = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = dict(line.rsplit(" ", 1) for line in lines if line)
+    structs = {"PckGemv": _lib.PckGemv, "PckCheckDesc": _lib.PckCheckDesc, "PckCheckBatch": _lib.PckCheckBatch}
+    for key, value in got.items():
+        if "." in key:
+            struct, field = key.split(".")
+            assert getattr(structs[struct], field).offset == int(value), key
+        else:
+            assert ctypes.sizeof(structs[key]) == int(value), key
