@@ -7,11 +7,22 @@ seven outputs at block b = 128, K = 1.  Weights are random (the reference's gene
 N(0, 0.02) BF16, x ~ N(0, 1) BF16) and rotate over several distinct layer copies whose total
 exceeds L2 + MALL, so every step streams its weights from HBM, as decoding through a model does.
 
+A 32-layer decode pass (the depth of Llama-3-8B) cycling over the layer copies is captured once
+in a HIP graph and replayed, as a decode loop replays its captured model (eager Python launches
+leave the GPU idle between kernels; their per-step time is reported beside).  Every GEMV output
+is checked by the trusted blocked checker in a later launch of the same stream: the checker's
+workgroups ride in the next GEMV launch (pck_gemv_group_check; bit-identical to a standalone
+check), so their latency hides behind the weight stream.  The same pass with one standalone
+checker launch per layer (the reference's batched mode) is reported as
+checker_overhead_serial_pct, and with that launch on a side stream as
+checker_overhead_side_stream_pct.
+
 Printed JSON line:
-  value          GEMV algorithmic bytes per step / time per step, checker included (GB/s)
+  value          GEMV algorithmic bytes per step / time per replayed step, checker included
   roofline       the dominant kernel (the BF16 tree GEMV instance used by q/k/v, o, gate/up):
-                 algorithmic bytes per launch / its mean launch duration from HIP events
-                 recorded around each launch on the launch stream, against 8 TB/s
+                 algorithmic bytes per launch / its mean launch duration, from HIP events on
+                 the launch stream around a graph that replays those launches back to back
+                 over every layer copy, against 8 TB/s
   cpu_baseline   the oracle's CPU model of the same work (coalesced-tree GEMV + CPU blocked
                  checker) timed on this host on a bounded sample
 plus the FP8 layer, GEMV-only times, the checker overhead and a read-only stream ceiling.
@@ -101,6 +112,141 @@ def run_step(layer, with_check: bool, events=None):  # type: ignore[no-untyped-d
     return outs, None
 
 
+MODE_GEMV, MODE_SERIAL, MODE_OVERLAP, MODE_RIDE = "gemv", "serial", "overlapped", "carried"
+
+# In carried mode each launch of layer L also checks outputs finished by earlier launches:
+# o carries q/k/v's checks, gate_up carries o's, down carries gate/up's, and the next layer's
+# qkv carries down's (the pass ends with one standalone check of the last down).
+CARRIES = {"qkv": ("down",), "o": ("q", "k", "v"), "gate_up": ("o",), "down": ("gate", "up")}
+
+
+def ride_pass(layers, depth: int):  # type: ignore[no-untyped-def]
+    """One decode pass of ``depth`` layers in carried mode; returns every check result."""
+    from pck.cuda import check_many, gemv_group_check
+
+    results = []
+    prev = None  # (layer, outputs) of the previous layer
+    for i in range(depth):
+        layer = layers[i % len(layers)]
+        outs = {}
+        for launch, names in LAUNCHES:
+            if launch == "qkv":
+                src = prev
+            else:
+                src = (layer, outs)
+            checks = []
+            if src is not None:
+                owner, produced = src
+                checks = [(owner[n][2], owner[n][1], produced[n]) for n in CARRIES[launch]]
+            ys, res = gemv_group_check([(layer[n][0], layer[n][1]) for n in names], checks, THREADS)
+            results.extend(res)
+            outs.update(zip(names, ys))
+        prev = (layer, outs)
+    owner, produced = prev
+    results.extend(check_many([(owner["down"][2], owner["down"][1], produced["down"])]))
+    return results
+
+
+def capture(layers, mode: str, depth: int):  # type: ignore[no-untyped-def]
+    """One HIP graph holding a decode pass of ``depth`` layers (cycling over the layer copies).
+
+    gemv:        the GEMV launches only;
+    serial:      each layer's checker launch follows its GEMVs on the same stream;
+    overlapped:  each layer's checker launch runs on a side stream once that layer's last GEMV
+                 has finished, concurrently with the next layer's GEMVs (the reference's
+                 SideStreamChecker pattern); the pass ends when the last check has.
+    Only this library's kernels are captured (no memset, no library reduction)."""
+    import torch
+
+    from pck.cuda import check_many
+
+    main = torch.cuda.current_stream()
+    side = torch.cuda.Stream()
+    warm = torch.cuda.Stream()
+    warm.wait_stream(main)
+    with torch.cuda.stream(warm):
+        for layer in layers:
+            run_step(layer, mode != MODE_GEMV)  # warm the allocator outside capture
+    main.wait_stream(warm)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    keep = []
+    if mode == MODE_RIDE:
+        with torch.cuda.graph(graph):
+            keep.append(ride_pass(layers, depth))
+        torch.cuda.synchronize()
+        return graph, keep
+    with torch.cuda.graph(graph):
+        cap = torch.cuda.current_stream()
+        for i in range(depth):
+            layer = layers[i % len(layers)]
+            outs, _ = run_step(layer, mode == MODE_SERIAL)
+            keep.append(outs)
+            if mode == MODE_OVERLAP:
+                ready = torch.cuda.Event()
+                ready.record(cap)
+                side.wait_event(ready)
+                with torch.cuda.stream(side):
+                    keep.append(check_many([(layer[n][2], layer[n][1], outs[n]) for n, _, _ in LAYER]))
+        if mode == MODE_OVERLAP:
+            done = torch.cuda.Event()
+            done.record(side)
+            cap.wait_event(done)
+    torch.cuda.synchronize()
+    return graph, keep
+
+
+def timed_graph(graph, depth: int, reps: int) -> float:  # type: ignore[no-untyped-def]
+    """ms per layer of a captured pass replayed ``reps`` times."""
+    import torch
+
+    graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (reps * depth)
+
+
+def dominant_launch_ms(layers, reps: int) -> tuple[float, int]:  # type: ignore[no-untyped-def]
+    """Mean duration of the dominant kernel's launches (q/k/v, o, gate/up groups) replayed
+    back to back from one graph over every layer copy, and their mean algorithmic bytes."""
+    import torch
+
+    from pck.cuda import gemv_group
+
+    dom = [launch for launch in LAUNCHES if launch[0] != "down"]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for layer in layers:
+            for _, names in dom:
+                gemv_group([(layer[n][0], layer[n][1]) for n in names], THREADS)
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for layer in layers:
+            for _, names in dom:
+                gemv_group([(layer[n][0], layer[n][1]) for n in names], THREADS)
+    nbytes = sum(gemv_bytes(m, n, 2) for name, m, n in LAYER for _, names in dom if name in names)
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    launches = len(dom) * len(layers)
+    return start.elapsed_time(end) / (reps * launches), nbytes // len(dom)
+
+
 def timed(layers, steps: int, warmup: int, with_check: bool, per_kernel: bool):  # type: ignore[no-untyped-def]
     """(ms per step, {launch: [ms per launch]}) over ``steps`` steps after ``warmup``."""
     import torch
@@ -182,33 +328,47 @@ def main() -> None:
     }
     # correctness first: every check passes on the honest outputs
     _, results = run_step(bf16_layers[0], True)
+    args.steps = max(args.steps, 32)
     assert all(bool(r.verdict.all()) for r in results), "checker rejected an honest output"
 
-    print("[bench] timing BF16 layer", file=sys.stderr, flush=True)
-    ms_checked, per_launch = timed(bf16_layers, args.steps, args.warmup, True, per_kernel=True)
-    ms_events_free, _ = timed(bf16_layers, args.steps, args.warmup, True, per_kernel=False)
-    ms_gemv_only, _ = timed(bf16_layers, args.steps, args.warmup, False, per_kernel=False)
+    depth = 32  # a Llama-3-8B decode pass
+    reps = max(1, args.steps // depth)
+    print("[bench] timing BF16 passes (HIP graphs)", file=sys.stderr, flush=True)
+    ms = {}
+    for mode in (MODE_GEMV, MODE_SERIAL, MODE_OVERLAP, MODE_RIDE):
+        graph, keep = capture(bf16_layers, mode, depth)
+        ms[mode] = timed_graph(graph, depth, reps)
+        if mode in (MODE_OVERLAP, MODE_RIDE):
+            verdicts = [r for item in keep if isinstance(item, list) for r in item]
+            assert len(verdicts) == 7 * depth, len(verdicts)
+            assert all(bool(r.verdict.all()) for r in verdicts), "checker rejected an honest output"
+        del graph, keep
+    ms_eager, per_launch = timed(bf16_layers, args.steps, args.warmup, True, per_kernel=True)
+    dom_ms, dom_bytes = dominant_launch_ms(bf16_layers, max(10, args.steps // 10))
     del bf16_layers
     torch.cuda.empty_cache()
 
-    print("[bench] building and timing FP8 layer", file=sys.stderr, flush=True)
+    print("[bench] building and timing FP8 passes", file=sys.stderr, flush=True)
     fp8_layers = build_layers(args.copies, fp8=True, gen=gen)
     _, results = run_step(fp8_layers[0], True)
     assert all(bool(r.verdict.all()) for r in results), "checker rejected an honest FP8 output"
     bytes_fp8 = sum(gemv_bytes(m, n, 1) for _, m, n in LAYER)
-    fp8_checked, fp8_launch = timed(fp8_layers, args.steps, args.warmup, True, per_kernel=True)
-    fp8_gemv_only, _ = timed(fp8_layers, args.steps, args.warmup, False, per_kernel=False)
+    ms8 = {}
+    for mode in (MODE_GEMV, MODE_SERIAL, MODE_OVERLAP, MODE_RIDE):
+        graph, keep = capture(fp8_layers, mode, depth)
+        ms8[mode] = timed_graph(graph, depth, reps)
+        if mode == MODE_RIDE:
+            verdicts = [r for item in keep if isinstance(item, list) for r in item]
+            assert all(bool(r.verdict.all()) for r in verdicts), "checker rejected an honest output"
+        del graph, keep
     del fp8_layers
     torch.cuda.empty_cache()
+    ms_checked, ms_gemv_only = ms[MODE_RIDE], ms[MODE_GEMV]
+    fp8_checked, fp8_gemv_only = ms8[MODE_RIDE], ms8[MODE_GEMV]
 
     read_ceiling = read_bandwidth_gbps()
-
-    # Dominant kernel: the BF16 tree GEMV instance of the n = 4096 launches (q/k/v, o, gate/up).
-    dom = ("qkv", "o", "gate_up")
-    dom_ms = [t for name in dom for t in per_launch[name]]
-    dom_bytes = sum(launch_bytes[name] * len(per_launch[name]) for name in dom)
-    achieved = dom_bytes / (sum(dom_ms) / 1e3) / 1e9
-    value = bytes_bf16 / (ms_events_free / 1e3) / 1e9
+    achieved = dom_bytes / (dom_ms / 1e3) / 1e9
+    value = bytes_bf16 / (ms_checked / 1e3) / 1e9
 
     line = {
         "metric": "GEMV HBM GB/s (% of peak), BF16/FP8, Llama-3-8B shapes; checker overhead %",
@@ -217,33 +377,41 @@ def main() -> None:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_events_free, 5),
+        "ms_per_step": round(ms_checked, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16 x bf16 -> fp32 (checker fp64)",
         "data": "synthetic: reference generator, W ~ N(0, 0.02) bf16, x ~ N(0, 1) bf16",
         "config": {
-            "workload": "Llama-3-8B decode layer, batch 1: 7 BF16 GEMVs (4 launches) + 1 "
-            "blocked-checker launch, b=128, K=1, T=256",
+            "workload": "Llama-3-8B decode layer, batch 1: 7 BF16 GEMVs (4 launches), every "
+            "output checked by the blocked checker (b=128, K=1, T=256) in a later launch of the "
+            "pass; 32-layer passes replayed from a HIP graph",
             "layer_copies": args.copies,
             "gemv_bytes_per_step": bytes_bf16,
         },
         "pct_of_peak": round(100 * value / HBM_PEAK_GBPS, 2),
         "gemv_only_gbps": round(bytes_bf16 / (ms_gemv_only / 1e3) / 1e9, 1),
-        "checker_overhead_pct": round(100 * (ms_events_free / ms_gemv_only - 1), 2),
+        "checker_overhead_pct": round(100 * (ms_checked / ms_gemv_only - 1), 2),
+        "checker_overhead_serial_pct": round(100 * (ms[MODE_SERIAL] / ms_gemv_only - 1), 2),
+        "checker_overhead_side_stream_pct": round(100 * (ms[MODE_OVERLAP] / ms_gemv_only - 1), 2),
+        "eager_ms_per_step": round(ms_eager, 5),
         "fp8": {
             "value_gbps": round(bytes_fp8 / (fp8_checked / 1e3) / 1e9, 1),
             "gemv_only_gbps": round(bytes_fp8 / (fp8_gemv_only / 1e3) / 1e9, 1),
             "checker_overhead_pct": round(100 * (fp8_checked / fp8_gemv_only - 1), 2),
+            "checker_overhead_serial_pct": round(100 * (ms8[MODE_SERIAL] / fp8_gemv_only - 1), 2),
+            "checker_overhead_side_stream_pct": round(
+                100 * (ms8[MODE_OVERLAP] / fp8_gemv_only - 1), 2
+            ),
             "ms_per_step": round(fp8_checked, 5),
-            "launch_ms": {k: round(statistics.mean(v), 5) for k, v in fp8_launch.items()},
         },
-        "launch_ms": {k: round(statistics.mean(v), 5) for k, v in per_launch.items()},
+        "eager_launch_ms": {k: round(statistics.mean(v), 5) for k, v in per_launch.items()},
         "hbm_read_ceiling_gbps": round(read_ceiling, 1),
         "roofline": {
             "bound": "hbm",
-            "kernel": "gemv_tree_kernel<256,1,2,bf16> (q/k/v, o, gate/up launches)",
+            "kernel": "gemv_tree_kernel<256,1,2,bf16,nt> (q/k/v, o, gate/up launches)",
+            "launch_ms": round(dom_ms, 5),
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",

@@ -63,11 +63,25 @@ typedef struct PckGemv {
  * a grouped launch gives the same one-launch cost without the copy. */
 int pck_gemv_group(int weight_kind, const PckGemv* gemvs, int count, int threads, void* stream);
 
-/* Launch-shape knob of the coalesced kernels, for tuning sweeps: rows per wave slot (1 or 2) and
- * vector positions loaded ahead per lane; 0, 0 restores the built-in choice.  Changes only
- * speed: outputs keep the same bits for every shape.  Not thread-safe; no reference
+struct PckCheckBatch;
+
+/* pck_gemv_group plus the blocked checks of `ride` (NULL: none) in the same launch: the first
+ * workgroups of the grid run the checker's per-(check, block) work, the rest the GEMVs.  The
+ * checked outputs must come from launches earlier on `stream` (not from this one).  rho, tau
+ * and the verdicts are bit-identical to pck_blocked_check(ride); the checker workgroups are
+ * separate wavefronts reading y from memory, so a check never trusts the launch it rides in.
+ * At threads = 256 with vector loads the checks share the launch; otherwise they run as their
+ * own launch just before the GEMVs.  No reference counterpart: it hides the checker launch's
+ * fixed latency behind the GEMV stream (the reference's check_many is a separate launch). */
+int pck_gemv_group_check(int weight_kind, const PckGemv* gemvs, int count, int threads,
+                         const struct PckCheckBatch* ride, void* stream);
+
+/* Launch-shape knob of the coalesced kernels at threads = 256, for tuning sweeps: rows per wave
+ * slot (1, 2 or 4), vector positions loaded ahead per lane (1, 2 or 4) and non-temporal weight
+ * loads (0 or 1); rows_per_wave = 0 restores the built-in choice.  Changes only speed: outputs
+ * keep the same bits for every shape.  Process-wide and not thread-safe; no reference
  * counterpart. */
-int pck_gemv_set_shape(int rows_per_wave, int unroll);
+int pck_gemv_set_shape(int rows_per_wave, int unroll, int nontemporal);
 
 /* ---------------------------------------------------------------------------------------------
  * Blocked checksum checker.  Field for field the reference's CheckDesc / CheckBatch
@@ -83,8 +97,8 @@ typedef struct PckCheckDesc {
   const int8_t* r;         /* (K, nb, b) secret signs in {-1, +1}                     */
   const void* x;           /* (n,) BF16                                               */
   const float* y;          /* (nb * b,) FP32 output under check                       */
-  double* partial_cx;      /* (K, nb, segments) scratch                               */
-  double* partial_s;       /* (K, nb, segments) scratch                               */
+  double* partial_cx;      /* (K, nb, segments) scratch (unused by this kernel)         */
+  double* partial_s;       /* (K, nb, segments) scratch (unused by this kernel)         */
   unsigned int* counters;  /* (K, nb) zero on entry; left zero on exit                */
   uint8_t* passed;         /* (K, nb) outputs: bool, rho, tau                         */
   double* rho;
@@ -106,7 +120,10 @@ typedef struct PckCheckBatch {
   int32_t count;                    /* 1 .. PCK_MAX_BATCH */
 } PckCheckBatch;
 
-/* One launch checks every described output (K * nb * segments work items per check). */
+/* One launch checks every described output, one work item (a 512-lane workgroup) per
+ * (check, block) pair: start[g + 1] - start[g] = checks * num_blocks.  The scratch fields
+ * (partial_cx, partial_s, counters) and `segments` keep the reference's descriptor; the
+ * kernel reads and writes neither (counters stay zero). */
 int pck_blocked_check(const PckCheckBatch* batch, void* stream);
 
 /* ---------------------------------------------------------------------------------------------

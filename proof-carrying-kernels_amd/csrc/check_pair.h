@@ -1,0 +1,198 @@
+// The blocked checker's work for one (check, block) pair, by one 256-lane workgroup.  Shared by
+// the standalone checker kernel (checker.hip) and by GEMV launches that carry checks of outputs
+// produced by earlier launches (gemv.hip), so both give bit-identical rho, tau and verdicts.
+//
+// Bank (built at weight load by pck.cuda.checker, reference src/pck/cuda/checker.py:72-129):
+//   c[k, beta, :] = r[k, beta, :]^T W_beta     FP32, rounded to nearest
+//   a[beta, :]    = sum_{i in beta} |W_i|       BF16, rounded up
+//   r[k, beta, :] in {-1, +1}                   int8, secret
+// For every check k and row block beta (reference src/pck/cuda/csrc/checker_kernel.cu:49-91):
+//   rho = c . x - r . y_beta
+//   s   = a . |x|                               every operation rounded up, then up to FP32
+//   tau = coef s + geps ((1 + u32) s + sum |y_beta|) + tau_floor, every operation rounded up
+// and the block passes only if every y in it is finite, tau is finite and |rho| <= tau.
+//
+// Arithmetic.  FP64 runs at the FP32 (non-packed) rate on MI355X, so rho is evaluated entirely
+// in FP64: each c_j x_j (24 + 8 significand bits) is exact in FP64 and every addition is one
+// FP64 operation, so rho's rounding error is at most gamma_H(u64) (sum |c_j x_j| + sum |y_i|)
+// for the depth H <= n + b + 1 of its evaluation, which the host's geps (reference formula,
+// which also carries the reference's FP32 Dot2 term) covers.  s and the sums of |y| add exact
+// non-negative terms with error-free round-up additions; s is then rounded up to FP32 once, so
+// an a . |x| beyond the FP32 range gives s = inf, tau = inf and a failed block, the reference's
+// fail-closed overflow.  tau's products and sums use the general round-up operations.
+//
+// Order.  Lane t accumulates the y terms of rows t, t + 256, ..., then the bank quads t,
+// t + 256, t + 512, ... in increasing order (four accumulators per quantity, one per column of a
+// quad); the workgroup reduction is a fixed wave64 butterfly and a fixed halving over the four
+// waves.  The result does not depend on scheduling or on kAhead (loads issued ahead per lane).
+
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "pck_hip.h"
+#include "rounding.h"
+
+namespace pck {
+namespace check {
+
+constexpr int kThreads = 256;
+constexpr int kWave = 64;
+constexpr int kWaves = kThreads / kWave;
+constexpr double kOnePlusU32 = 1.0 + 0x1p-24;  // exact in FP64
+
+__device__ __forceinline__ double bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ double bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+__device__ __forceinline__ double bf16_at(const uint16_t* p, int64_t j) {
+  return __uint_as_float(static_cast<uint32_t>(p[j]) << 16);
+}
+
+// The smallest FP32 value >= v (v >= 0), widened back to FP64; +inf beyond the FP32 range.
+__device__ __forceinline__ double round_up_to_f32(double v) {
+  float f = static_cast<float>(v);
+  if (static_cast<double>(f) < v) f = __uint_as_float(__float_as_uint(f) + 1u);  // v >= 0
+  return static_cast<double>(f);
+}
+
+// The four per-lane quantities: c.x and r.y round to nearest, s and sum |y| round up.
+struct Quad {
+  double cx, s, ry, yabs;
+};
+
+__device__ __forceinline__ Quad combine(const Quad& a, const Quad& b) {
+  return Quad{a.cx + b.cx, add_up_nonneg(a.s, b.s), a.ry + b.ry, add_up_nonneg(a.yabs, b.yabs)};
+}
+
+// Workgroup sums of the four quantities in one exchange, valid in every lane.
+__device__ __forceinline__ Quad group_sum(Quad v, Quad* lds) {
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off /= 2) {
+    const Quad o{__shfl_xor(v.cx, off, kWave), __shfl_xor(v.s, off, kWave),
+                 __shfl_xor(v.ry, off, kWave), __shfl_xor(v.yabs, off, kWave)};
+    v = combine(v, o);  // symmetric in its operands: every lane holds the same value
+  }
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) lds[wave] = v;
+  __syncthreads();
+  Quad w[kWaves];
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) w[i] = lds[i];
+#pragma unroll
+  for (int half = kWaves / 2; half > 0; half /= 2)
+#pragma unroll
+    for (int i = 0; i < half; ++i) w[i] = combine(w[i], w[i + half]);
+  return w[0];
+}
+
+// One column: c.x with the exact product (one rounding, the add's) and a.|x| rounded up.
+__device__ __forceinline__ void column(double& cx, double& s, double cj, double aj, double xj) {
+  cx = __builtin_fma(cj, xj, cx);
+  s = add_up_nonneg(s, aj * __builtin_fabs(xj));
+}
+
+// Checks work item `item` of `batch` (one (check, block) pair) with the calling workgroup of
+// kThreads lanes; `lds` holds kWaves Quads.  Lane 0 writes passed, rho and tau.
+template <int kAhead>
+__device__ __forceinline__ void check_pair(const PckCheckBatch& batch, int64_t item, Quad* lds) {
+  int g = 0;
+  while (g + 1 < batch.count && item >= batch.start[g + 1]) ++g;
+  const PckCheckDesc& d = batch.desc[g];
+  const int64_t pair = item - batch.start[g];  // k * num_blocks + beta
+  const int64_t beta = pair % d.num_blocks;
+  const int64_t n = d.n;
+  const int t = static_cast<int>(threadIdx.x);
+  const float* c_row = d.c + pair * n;
+  const uint16_t* a_row = static_cast<const uint16_t*>(d.a) + beta * n;
+  const uint16_t* x = static_cast<const uint16_t*>(d.x);
+  const int8_t* r_row = d.r + pair * d.block;
+  const float* y_blk = d.y + beta * d.block;
+
+  // The y terms first: their loads are independent of the bank's.  A non-finite y makes
+  // sum |y| non-finite (FP32 values cannot overflow an FP64 sum of at most 2^31 of them).
+  Quad q{0.0, 0.0, 0.0, 0.0};
+  for (int i = t; i < d.block; i += kThreads) {
+    const double yd = static_cast<double>(y_blk[i]);
+    q.ry = q.ry + (r_row[i] > 0 ? yd : -yd);
+    q.yabs = add_up_nonneg(q.yabs, __builtin_fabs(yd));
+  }
+
+  // Bank terms: kAhead quads per lane are loaded before any is consumed; indices past the row
+  // load quad 0 and their columns are zeroed (c = x = 0 adds exactly nothing), so the loop has
+  // no data-dependent branches.
+  double cx[4] = {0.0, 0.0, 0.0, 0.0};
+  double sa[4] = {0.0, 0.0, 0.0, 0.0};
+  int64_t done = 0;
+  const bool quads = n % 4 == 0 && (reinterpret_cast<uintptr_t>(c_row) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(a_row) & 7) == 0 &&
+                     (reinterpret_cast<uintptr_t>(x) & 7) == 0;
+  if (quads) {
+    const float4* c4 = reinterpret_cast<const float4*>(c_row);
+    const uint2* a4 = reinterpret_cast<const uint2*>(a_row);
+    const uint2* x4 = reinterpret_cast<const uint2*>(x);
+    const int64_t nq = n / 4;
+    for (int64_t q0 = t; q0 < nq; q0 += kAhead * kThreads) {
+      float4 cv[kAhead];
+      uint2 av[kAhead];
+      uint2 xv[kAhead];
+#pragma unroll
+      for (int k = 0; k < kAhead; ++k) {
+        const int64_t qk = q0 + static_cast<int64_t>(k) * kThreads;
+        const int64_t at = qk < nq ? qk : 0;
+        cv[k] = c4[at];
+        av[k] = a4[at];
+        xv[k] = x4[at];
+      }
+#pragma unroll
+      for (int k = 0; k < kAhead; ++k) {
+        const bool in = q0 + static_cast<int64_t>(k) * kThreads < nq;
+        const float4 c = in ? cv[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const uint2 xx = in ? xv[k] : make_uint2(0u, 0u);
+        column(cx[0], sa[0], c.x, bf16_lo(av[k].x), bf16_lo(xx.x));
+        column(cx[1], sa[1], c.y, bf16_hi(av[k].x), bf16_hi(xx.x));
+        column(cx[2], sa[2], c.z, bf16_lo(av[k].y), bf16_lo(xx.y));
+        column(cx[3], sa[3], c.w, bf16_hi(av[k].y), bf16_hi(xx.y));
+      }
+    }
+    done = nq * 4;
+  }
+  for (int64_t j = done + t; j < n; j += kThreads) {
+    column(cx[j & 3], sa[j & 3], static_cast<double>(c_row[j]), bf16_at(a_row, j), bf16_at(x, j));
+  }
+  q.cx = (cx[0] + cx[2]) + (cx[1] + cx[3]);
+  q.s = add_up_nonneg(add_up_nonneg(sa[0], sa[2]), add_up_nonneg(sa[1], sa[3]));
+
+  const Quad total = group_sum(q, lds);
+  if (t == 0) {
+    const double s_up = round_up_to_f32(total.s);
+    const double rho = total.cx - total.ry;
+    const double cabs_up = mul_up(kOnePlusU32, s_up);
+    const double eps = mul_up(d.geps, add_up(cabs_up, total.yabs));
+    const double tau = add_up(add_up(mul_up(d.coef, s_up), eps), d.tau_floor);
+    // Non-finite outputs and an overflowing threshold (tau = inf) fail closed; NaN compares
+    // false.
+    d.passed[pair] =
+        __builtin_isfinite(total.yabs) && __builtin_isfinite(tau) && __builtin_fabs(rho) <= tau;
+    d.rho[pair] = rho;
+    d.tau[pair] = tau;
+  }
+}
+
+// Host-side validation of a batch: the shape of every descriptor and the work-item prefix sums
+// (one item per (check, block) pair).  Returns hipSuccess or hipErrorInvalidValue.
+inline hipError_t validate(const PckCheckBatch& batch) {
+  if (batch.count < 1 || batch.count > PCK_MAX_BATCH || batch.start[0] != 0)
+    return hipErrorInvalidValue;
+  for (int g = 0; g < batch.count; ++g) {
+    const PckCheckDesc& d = batch.desc[g];
+    if (d.num_blocks < 1 || d.checks < 1 || d.block < 1 || d.n < 1 || !d.c || !d.a || !d.r ||
+        !d.x || !d.y || !d.passed || !d.rho || !d.tau ||
+        batch.start[g + 1] - batch.start[g] != static_cast<int64_t>(d.checks) * d.num_blocks)
+      return hipErrorInvalidValue;
+  }
+  return hipSuccess;
+}
+
+}  // namespace check
+}  // namespace pck

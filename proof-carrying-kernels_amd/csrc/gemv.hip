@@ -30,6 +30,7 @@
 
 #include <cstdint>
 
+#include "check_pair.h"
 #include "pck_hip.h"
 
 namespace pck {
@@ -123,18 +124,50 @@ __device__ __forceinline__ void add_products_scalar(float& acc, const void* w_ro
   }
 }
 
-__device__ __forceinline__ float xor32(float v, int offset) { return __shfl_xor(v, offset, kWarp); }
+// a[i] += a[i + 16] ... a[0] += a[1] inside each 32-lane half of the wave, the halving order of
+// the reference's 32-lane shuffle-down reduction, with lane 0 (and lane 32) ending on a[0].
+// Step 16 moves whole rows of 16 lanes with gfx950's v_permlane16_swap (the second result holds
+// each even row's partner row); steps 8 and 4 rotate inside a row (row_ror:8 gives lane i the
+// value of lane i ^ 8, row_ror:12 that of lane i + 4 for the lanes i < 4 that matter); steps 2
+// and 1 are quad permutes.  Everything stays in VALU instructions (DPP folds into the adds).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float halve32(float v) {
+  const auto swapped = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false,
+                                                        false);
+  v = v + __int_as_float(swapped[1]);  // lanes 0-15 (32-47) receive lanes 16-31 (48-63)
+  v = v + dpp_move<0x128>(v);          // row_ror:8
+  v = v + dpp_move<0x12C>(v);          // row_ror:12
+  v = v + dpp_move<0x4E>(v);           // quad_perm [2,3,0,1]
+  v = v + dpp_move<0xB1>(v);           // quad_perm [1,0,3,2]
+  return v;
+}
 
 __device__ __forceinline__ float lane_value(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
-// T virtual lanes per row, R rows per wave slot, U vector positions loaded ahead.
+// T virtual lanes per row, R rows per wave slot, U vector positions loaded ahead, kNt:
+// non-temporal weight loads (streamed once, so they need not displace x in the caches).
 // kPad: some vectors of a chain lie past n (n is not a multiple of T * vec), so loads of those
 // are redirected to column 0 and their data replaced by zeros.  kVector: 16-byte loads (n is a
 // multiple of vec and the pointers are aligned); otherwise element loads.
-template <int T, int R, int U, bool kFp8, bool kVector, bool kPad>
-__global__ void __launch_bounds__(kGroupThreads) gemv_tree_kernel(const GemvBatch batch) {
+template <bool kNt>
+__device__ __forceinline__ uint4 load_w(const unsigned char* p) {
+  if constexpr (kNt) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v[0], v[1], v[2], v[3]);
+  } else {
+    return *reinterpret_cast<const uint4*>(p);
+  }
+}
+
+template <int T, int R, int U, bool kFp8, bool kVector, bool kPad, bool kNt>
+__device__ __forceinline__ void gemv_rows(const GemvBatch& batch, int64_t group) {
   constexpr int V = kFp8 ? 16 : 8;
   constexpr int kLanesPerRow = T >= kWave ? kWave : T;
   constexpr int kSlots = kWave / kLanesPerRow;  // rows side by side in one wave (2 if T = 32)
@@ -142,12 +175,11 @@ __global__ void __launch_bounds__(kGroupThreads) gemv_tree_kernel(const GemvBatc
   constexpr int kElemBytes = kFp8 ? 1 : 2;
 
   int g = 0;
-  while (g + 1 < batch.count && static_cast<int64_t>(blockIdx.x) >= batch.first_group[g + 1]) ++g;
+  while (g + 1 < batch.count && group >= batch.first_group[g + 1]) ++g;
   const GemvItem& it = batch.item[g];
   const int lane = static_cast<int>(threadIdx.x) & (kWave - 1);
   const int64_t wave =
-      (static_cast<int64_t>(blockIdx.x) - batch.first_group[g]) * kWavesPerGroup +
-      (static_cast<int>(threadIdx.x) >> 6);
+      (group - batch.first_group[g]) * kWavesPerGroup + (static_cast<int>(threadIdx.x) >> 6);
   const int slot = lane / kLanesPerRow;
   const int chain0 = lane % kLanesPerRow;
   const int64_t n = it.n;
@@ -187,7 +219,7 @@ __global__ void __launch_bounds__(kGroupThreads) gemv_tree_kernel(const GemvBatc
           if constexpr (kFp8) xb[u][j] = *reinterpret_cast<const uint4*>(x + at + 8);
 #pragma unroll
           for (int r = 0; r < R; ++r)
-            wb[u][r][j] = *reinterpret_cast<const uint4*>(w_rows[r] + at * kElemBytes);
+            wb[u][r][j] = load_w<kNt>(w_rows[r] + at * kElemBytes);
           if constexpr (kPad) {
             if (col >= n) {  // a padding vector: +0 products (0 x 0)
               xa[u][j] = make_uint4(0, 0, 0, 0);
@@ -221,13 +253,9 @@ __global__ void __launch_bounds__(kGroupThreads) gemv_tree_kernel(const GemvBatc
 
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    // Halving inside each 32-lane virtual warp (width-32 xor butterfly: lane 0 of each half
-    // holds a[0] after a[i] += a[i + 16], a[i] += a[i + 8], ..., a[0] += a[1]).
+    // Halving inside each 32-lane virtual warp.
 #pragma unroll
-    for (int j = 0; j < kChains; ++j) {
-#pragma unroll
-      for (int off = kWarp / 2; off > 0; off /= 2) acc[r][j] = acc[r][j] + xor32(acc[r][j], off);
-    }
+    for (int j = 0; j < kChains; ++j) acc[r][j] = halve32(acc[r][j]);
     const int64_t row = (wave * kSlots + slot) * R + r;
     if constexpr (kSlots == 2) {
       // T = 32: one virtual warp per row; lanes 0 and 32 hold the two rows' sums.
@@ -248,6 +276,29 @@ __global__ void __launch_bounds__(kGroupThreads) gemv_tree_kernel(const GemvBatc
       if (lane == 0 && live[r]) it.y[row] = ws[0];
     }
   }
+}
+
+template <int T, int R, int U, bool kFp8, bool kVector, bool kPad, bool kNt>
+__global__ void __launch_bounds__(kGroupThreads) gemv_tree_kernel(const GemvBatch batch) {
+  gemv_rows<T, R, U, kFp8, kVector, kPad, kNt>(batch, blockIdx.x);
+}
+
+// A GEMV launch that also checks outputs of earlier launches: the first workgroups of the grid
+// each run one (check, block) pair of `ride` (the standalone checker's code, so rho, tau and the
+// verdicts are bit-identical to pck_blocked_check), the rest compute the GEMV rows.  The checked
+// y were written by launches that finished before this one started (stream order), and the
+// checker workgroups are separate wavefronts that read them from memory; their latency hides
+// behind the GEMV's streaming, and the bank reads add about 2.3% (BF16, b = 128) to the bytes.
+template <int T, int R, int U, bool kFp8, bool kPad, bool kNt>
+__global__ void __launch_bounds__(kGroupThreads)
+    gemv_ride_kernel(const GemvBatch batch, const PckCheckBatch ride) {
+  __shared__ check::Quad lds[check::kWaves];
+  const int64_t items = ride.start[ride.count];
+  if (static_cast<int64_t>(blockIdx.x) < items) {
+    check::check_pair<4>(ride, blockIdx.x, lds);
+    return;
+  }
+  gemv_rows<T, R, U, kFp8, true, kPad, kNt>(batch, static_cast<int64_t>(blockIdx.x) - items);
 }
 
 // Naive tree: one workgroup of `threads` lanes per row (reference gemv_kernel.cu:27-55).
@@ -274,54 +325,113 @@ __global__ void __launch_bounds__(1024)
   if (t == 0) y[blockIdx.x] = partial[0];
 }
 
-// Launch shape of the coalesced kernel: rows per wave slot and vector positions loaded ahead.
+// Launch shape of the coalesced kernel: rows per wave slot, vector positions loaded ahead and
+// non-temporal weight loads.  T = 256 (the reference's default tree) has every combination
+// instantiated for tuning; other thread counts use one shape per padding / weight type.
 struct TreeShape {
   int rows;
   int unroll;
+  int nt;
 };
 
-TreeShape g_shape_override = {0, 0};
+TreeShape g_shape_override = {0, 0, 0};
 
-TreeShape choose_shape(int threads, int64_t per_lane) {
+// Defaults from a sweep of every shape over the Llama-3-8B decode launches on MI355X
+// (non-temporal weight loads won everywhere; FP8 rows are half as long, so two rows per wave
+// keep as many bytes in flight as one BF16 row).
+TreeShape choose_shape(int64_t per_lane, bool fp8) {
   if (g_shape_override.rows > 0) return g_shape_override;
-  (void)threads;
-  return TreeShape{1, per_lane >= 4 ? 4 : 2};
+  if (fp8) return TreeShape{2, 1, 1};
+  return per_lane > 2 ? TreeShape{2, 2, 1} : TreeShape{1, 2, 1};
 }
 
-template <int T, int R, int U, bool kFp8, bool kVector, bool kPad>
-hipError_t launch_tree(GemvBatch& batch, hipStream_t stream) {
-  constexpr int kLanesPerRow = T >= kWave ? kWave : T;
-  constexpr int64_t kRowsPerGroup = (kWave / kLanesPerRow) * R * kWavesPerGroup;
+// Fills the workgroup prefix sums for rows_per_group rows per workgroup; returns the total.
+int64_t plan_groups(GemvBatch& batch, int64_t rows_per_group) {
   batch.first_group[0] = 0;
   for (int g = 0; g < batch.count; ++g) {
     batch.first_group[g + 1] =
-        batch.first_group[g] + (batch.item[g].m + kRowsPerGroup - 1) / kRowsPerGroup;
+        batch.first_group[g] + (batch.item[g].m + rows_per_group - 1) / rows_per_group;
   }
-  const int64_t groups = batch.first_group[batch.count];
+  return batch.first_group[batch.count];
+}
+
+template <int T, int R, int U, bool kFp8, bool kVector, bool kPad, bool kNt>
+hipError_t launch_tree(GemvBatch& batch, hipStream_t stream) {
+  constexpr int kLanesPerRow = T >= kWave ? kWave : T;
+  const int64_t groups = plan_groups(batch, (kWave / kLanesPerRow) * R * kWavesPerGroup);
   if (groups == 0) return hipSuccess;
   if (groups * kGroupThreads > 0xFFFFFFFFll) return hipErrorInvalidValue;  // 32-bit dispatch size
-  gemv_tree_kernel<T, R, U, kFp8, kVector, kPad>
+  gemv_tree_kernel<T, R, U, kFp8, kVector, kPad, kNt>
       <<<dim3(static_cast<unsigned>(groups)), dim3(kGroupThreads), 0, stream>>>(batch);
   return hipGetLastError();
 }
 
+template <int T, int R, bool kFp8, bool kPad, bool kNt>
+hipError_t launch_unroll(GemvBatch& batch, int unroll, hipStream_t s) {
+  if (unroll >= 4) return launch_tree<T, R, 4, kFp8, true, kPad, kNt>(batch, s);
+  if (unroll == 2) return launch_tree<T, R, 2, kFp8, true, kPad, kNt>(batch, s);
+  return launch_tree<T, R, 1, kFp8, true, kPad, kNt>(batch, s);
+}
+
 template <int T, bool kFp8, bool kPad>
 hipError_t launch_vector(GemvBatch& batch, TreeShape shape, hipStream_t s) {
-  if (shape.rows == 2) return launch_tree<T, 2, 2, kFp8, true, kPad>(batch, s);
-  if (shape.unroll >= 4) return launch_tree<T, 1, 4, kFp8, true, kPad>(batch, s);
-  return launch_tree<T, 1, 2, kFp8, true, kPad>(batch, s);
+  if constexpr (T == 256) {
+    const bool nt = shape.nt != 0;
+    switch (shape.rows) {
+      case 4:
+        return nt ? launch_unroll<T, 4, kFp8, kPad, true>(batch, shape.unroll, s)
+                  : launch_unroll<T, 4, kFp8, kPad, false>(batch, shape.unroll, s);
+      case 2:
+        return nt ? launch_unroll<T, 2, kFp8, kPad, true>(batch, shape.unroll, s)
+                  : launch_unroll<T, 2, kFp8, kPad, false>(batch, shape.unroll, s);
+      default:
+        return nt ? launch_unroll<T, 1, kFp8, kPad, true>(batch, shape.unroll, s)
+                  : launch_unroll<T, 1, kFp8, kPad, false>(batch, shape.unroll, s);
+    }
+  } else {
+    (void)shape;
+    return launch_tree<T, 1, 2, kFp8, true, kPad, false>(batch, s);
+  }
 }
 
 template <int T, bool kFp8>
 hipError_t launch_for_threads(GemvBatch& batch, bool vector, bool pad, TreeShape shape,
                               hipStream_t s) {
-  if (!vector) return launch_tree<T, 1, 1, kFp8, false, true>(batch, s);
+  if (!vector) return launch_tree<T, 1, 1, kFp8, false, true, false>(batch, s);
   return pad ? launch_vector<T, kFp8, true>(batch, shape, s)
              : launch_vector<T, kFp8, false>(batch, shape, s);
 }
 
+template <int R, int U, bool kFp8, bool kPad>
+hipError_t launch_ride_shape(GemvBatch& batch, const PckCheckBatch& ride, hipStream_t stream) {
+  const int64_t groups = plan_groups(batch, static_cast<int64_t>(R) * kWavesPerGroup);
+  const int64_t total = groups + ride.start[ride.count];
+  if (total * kGroupThreads > 0xFFFFFFFFll) return hipErrorInvalidValue;  // 32-bit dispatch size
+  gemv_ride_kernel<256, R, U, kFp8, kPad, true>
+      <<<dim3(static_cast<unsigned>(total)), dim3(kGroupThreads), 0, stream>>>(batch, ride);
+  return hipGetLastError();
+}
+
+// The carried-check launch uses the built-in shape of the T = 256 vector path.
 template <bool kFp8>
-hipError_t launch_group(const PckGemv* gemvs, int count, int threads, hipStream_t stream) {
+hipError_t launch_ride(GemvBatch& batch, bool pad, int64_t per_lane, const PckCheckBatch& ride,
+                       hipStream_t stream) {
+  if constexpr (kFp8) {
+    return pad ? launch_ride_shape<2, 1, true, true>(batch, ride, stream)
+               : launch_ride_shape<2, 1, true, false>(batch, ride, stream);
+  } else {
+    if (per_lane > 2) {
+      return pad ? launch_ride_shape<2, 2, false, true>(batch, ride, stream)
+                 : launch_ride_shape<2, 2, false, false>(batch, ride, stream);
+    }
+    return pad ? launch_ride_shape<1, 2, false, true>(batch, ride, stream)
+               : launch_ride_shape<1, 2, false, false>(batch, ride, stream);
+  }
+}
+
+template <bool kFp8>
+hipError_t launch_group(const PckGemv* gemvs, int count, int threads, const PckCheckBatch* ride,
+                        hipStream_t stream) {
   constexpr int V = kFp8 ? 16 : 8;
   if (count < 1 || count > PCK_MAX_GROUP || gemvs == nullptr) return hipErrorInvalidValue;
   if (threads < kWarp || threads > 1024 || (threads & (threads - 1)) != 0)
@@ -345,7 +455,20 @@ hipError_t launch_group(const PckGemv* gemvs, int count, int threads, hipStream_
       pad = pad || n % (static_cast<int64_t>(threads) * V) != 0;
     }
   }
-  const TreeShape shape = choose_shape(threads, max_per_lane);
+  if (ride != nullptr) {
+    if (check::validate(*ride) != hipSuccess) return hipErrorInvalidValue;
+    if (threads == 256 && vector) {
+      bool any_rows = false;
+      for (int g = 0; g < count; ++g) any_rows = any_rows || batch.item[g].m > 0;
+      if (any_rows) return launch_ride<kFp8>(batch, pad, max_per_lane, *ride, stream);
+    }
+    // Other configurations: the same check as its own launch first (identical results).
+    const int64_t items = ride->start[ride->count];
+    if (items * check::kThreads > 0xFFFFFFFFll) return hipErrorInvalidValue;
+    const int err = pck_blocked_check(ride, stream);
+    if (err != 0) return static_cast<hipError_t>(err);
+  }
+  const TreeShape shape = choose_shape(max_per_lane, kFp8);
   switch (threads) {
     case 32: return launch_for_threads<32, kFp8>(batch, vector, pad, shape, stream);
     case 64: return launch_for_threads<64, kFp8>(batch, vector, pad, shape, stream);
@@ -364,21 +487,25 @@ extern "C" {
 int pck_gemv_bf16_coalesced(const void* W, const void* x, float* y, int64_t m, int64_t n,
                             int threads, void* stream) {
   const PckGemv one{W, x, y, m, n};
-  return pck::launch_group<false>(&one, 1, threads, static_cast<hipStream_t>(stream));
+  return pck::launch_group<false>(&one, 1, threads, nullptr, static_cast<hipStream_t>(stream));
 }
 
 int pck_gemv_fp8_coalesced(const void* Q, const void* x, float* z, int64_t m, int64_t n,
                            int threads, void* stream) {
   const PckGemv one{Q, x, z, m, n};
-  return pck::launch_group<true>(&one, 1, threads, static_cast<hipStream_t>(stream));
+  return pck::launch_group<true>(&one, 1, threads, nullptr, static_cast<hipStream_t>(stream));
+}
+
+int pck_gemv_group_check(int weight_kind, const PckGemv* gemvs, int count, int threads,
+                         const PckCheckBatch* ride, void* stream) {
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (weight_kind == 0) return pck::launch_group<false>(gemvs, count, threads, ride, s);
+  if (weight_kind == 1) return pck::launch_group<true>(gemvs, count, threads, ride, s);
+  return hipErrorInvalidValue;
 }
 
 int pck_gemv_group(int weight_kind, const PckGemv* gemvs, int count, int threads, void* stream) {
-  if (weight_kind == 0)
-    return pck::launch_group<false>(gemvs, count, threads, static_cast<hipStream_t>(stream));
-  if (weight_kind == 1)
-    return pck::launch_group<true>(gemvs, count, threads, static_cast<hipStream_t>(stream));
-  return hipErrorInvalidValue;
+  return pck_gemv_group_check(weight_kind, gemvs, count, threads, nullptr, stream);
 }
 
 int pck_gemv_bf16_naive(const void* W, const void* x, float* y, int64_t m, int64_t n, int threads,
@@ -395,9 +522,11 @@ int pck_gemv_bf16_naive(const void* W, const void* x, float* y, int64_t m, int64
   return hipGetLastError();
 }
 
-int pck_gemv_set_shape(int rows_per_wave, int unroll) {
-  if (rows_per_wave < 0 || rows_per_wave > 2 || unroll < 0) return hipErrorInvalidValue;
-  pck::g_shape_override = pck::TreeShape{rows_per_wave, unroll};
+int pck_gemv_set_shape(int rows_per_wave, int unroll, int nontemporal) {
+  if (rows_per_wave < 0 || rows_per_wave > 4 || rows_per_wave == 3 || unroll < 0 || unroll > 4 ||
+      (rows_per_wave > 0 && unroll < 1))
+    return hipErrorInvalidValue;
+  pck::g_shape_override = pck::TreeShape{rows_per_wave, unroll, nontemporal != 0};
   return hipSuccess;
 }
 

@@ -1,6 +1,6 @@
 // Read-only streaming kernel: the practical HBM read ceiling the GEMV bandwidth is compared with.
 //
-// Every lane reads 16-byte vectors in a grid-stride loop (four in flight per iteration) and folds
+// Every lane reads 16-byte vectors in a grid-stride loop (eight non-temporal loads in flight per iteration) and folds
 // them with XOR; one value per workgroup is stored so the loads cannot be removed.  No reference
 // counterpart: the reference compares with a device-to-device copy (read + write,
 // src/pck/cuda/timing.py:50-55), which on MI355X understates a read-only stream.
@@ -21,13 +21,17 @@ __global__ void __launch_bounds__(kThreads)
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
   int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   uint32_t acc = 0;
-  for (; i + 3 * stride < vectors; i += 4 * stride) {
-    const uint4 a = src[i];
-    const uint4 b = src[i + stride];
-    const uint4 c = src[i + 2 * stride];
-    const uint4 d = src[i + 3 * stride];
-    acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w;
-    acc ^= c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^ d.z ^ d.w;
+  constexpr int kAhead = 8;
+  for (; i + (kAhead - 1) * stride < vectors; i += kAhead * stride) {
+    uint4 v[kAhead];
+#pragma unroll
+    for (int k = 0; k < kAhead; ++k) {
+      typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+      const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + i + k * stride));
+      v[k] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+#pragma unroll
+    for (int k = 0; k < kAhead; ++k) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
   }
   for (; i < vectors; i += stride) {
     const uint4 a = src[i];

@@ -58,3 +58,18 @@ __device__ __forceinline__ double mul_up(double a, double b) {
 }
 
 }  // namespace pck
+
+namespace pck {
+
+// RU(a + b) for a, b >= 0 without branches (the checkers' sums of magnitudes): the TwoSum
+// error decides whether the round-to-nearest sum is raised by one ulp; +inf stays +inf (its
+// error is NaN, which compares false); 0 + 0 stays +0.
+__device__ __forceinline__ double add_up_nonneg(double a, double b) {
+  const double s = a + b;
+  const double bv = s - a;
+  const double err = (a - (s - bv)) + (b - bv);
+  const double raised = __longlong_as_double(__double_as_longlong(s) + 1);
+  return err > 0.0 ? raised : s;
+}
+
+}  // namespace pck

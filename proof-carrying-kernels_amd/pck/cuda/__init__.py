@@ -11,7 +11,14 @@ from pck.cuda.checker import (
     check_many,
     round_up_bf16,
 )
-from pck.cuda.gemv import gemv_coalesced, gemv_fp8, gemv_group, gemv_naive, quantize_fp8
+from pck.cuda.gemv import (
+    gemv_coalesced,
+    gemv_fp8,
+    gemv_group,
+    gemv_group_check,
+    gemv_naive,
+    quantize_fp8,
+)
 
 __all__ = [
     "DEFAULT_BLOCK",
@@ -23,6 +30,7 @@ __all__ = [
     "gemv_coalesced",
     "gemv_fp8",
     "gemv_group",
+    "gemv_group_check",
     "gemv_naive",
     "quantize_fp8",
     "round_up_bf16",

@@ -70,7 +70,8 @@ SIGNATURES: dict[str, list[Any]] = {
     "pck_gemv_bf16_coalesced": [_p, _p, _p, _i64, _i64, _int, _p],
     "pck_gemv_fp8_coalesced": [_p, _p, _p, _i64, _i64, _int, _p],
     "pck_gemv_group": [_int, ctypes.POINTER(PckGemv), _int, _int, _p],
-    "pck_gemv_set_shape": [_int, _int],
+    "pck_gemv_group_check": [_int, ctypes.POINTER(PckGemv), _int, _int, _p, _p],
+    "pck_gemv_set_shape": [_int, _int, _int],
     "pck_blocked_check": [ctypes.POINTER(PckCheckBatch), _p],
     "pck_read_stream": [_p, _i64, _p, _int, _p],
     "pck_check_members": [

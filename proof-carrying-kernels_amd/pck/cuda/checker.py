@@ -76,9 +76,11 @@ class GpuBlockedChecker:
     (reference `src/pck/cuda/checker.py:60-137`).
 
     ``height`` is the summation-tree height of the GEMV being checked (e.g.
-    ``tree_height(n, threads, vec)``).  ``segments`` splits each block's n columns over that
-    many workgroups (default about ``BLOCKS_PER_SM`` per CU).  A checker owns its scratch, so
-    use it from one stream at a time.
+    ``tree_height(n, threads, vec)``).  ``segments`` and the scratch arrays keep the reference's
+    interface and validation (default about ``BLOCKS_PER_SM`` workgroups per CU); the HIP
+    kernel gives each (check, block) pair one workgroup over all n columns, so the value does
+    not change the launch, and the result does not depend on it.  Use a checker from one stream
+    at a time, as in the reference.
     """
 
     def __init__(
@@ -218,17 +220,15 @@ def _describe(
     return desc, (passed, rho, tau)
 
 
-def blocked_check(
+def build_batch(
     c: Sequence[torch.Tensor], a: Sequence[torch.Tensor], r: Sequence[torch.Tensor],
     x: Sequence[torch.Tensor], y: Sequence[torch.Tensor], partial_cx: Sequence[torch.Tensor],
     partial_s: Sequence[torch.Tensor], counters: Sequence[torch.Tensor], coef: Sequence[float],
     geps: Sequence[float], tau_floor: Sequence[float],
-) -> list[tuple[torch.Tensor, torch.Tensor, torch.Tensor]]:  # fmt: skip
-    """Checks up to eight GEMV outputs in one launch; (passed, rho, tau) per check.
-
-    The native entry of the reference's extension (`bindings.cpp:221-256`): same argument
-    lists, validation order and messages; the launch goes to `pck_blocked_check`.
-    """
+) -> tuple[PckCheckBatch, list[tuple[torch.Tensor, torch.Tensor, torch.Tensor]], torch.device]:  # fmt: skip
+    """Validates up to eight checks (reference `bindings.cpp:221-256`: same argument lists,
+    order and messages) and returns the launch descriptor, the freshly allocated outputs
+    (passed, rho, tau) of each check, and the device."""
     count = len(c)
     if not 1 <= count <= MAX_BATCH:
         raise RuntimeError(f"batch size must be in [1, {MAX_BATCH}], got {count}")
@@ -238,7 +238,6 @@ def blocked_check(
     if not y[0].is_cuda:
         raise RuntimeError("y must be a CUDA tensor")
     device = y[0].device
-    handle = lib()
     batch = PckCheckBatch()
     batch.count = count
     outputs = []
@@ -250,14 +249,53 @@ def blocked_check(
             geps[g], tau_floor[g], device,
         )  # fmt: skip
         batch.desc[g] = desc
-        batch.start[g + 1] = batch.start[g] + desc.checks * desc.num_blocks * desc.segments
+        batch.start[g + 1] = batch.start[g] + desc.checks * desc.num_blocks  # one per pair
         outputs.append(out)
     if batch.start[count] > 2**31 - 1:
         raise RuntimeError("too many blocks")
+    return batch, outputs, device
+
+
+def blocked_check(
+    c: Sequence[torch.Tensor], a: Sequence[torch.Tensor], r: Sequence[torch.Tensor],
+    x: Sequence[torch.Tensor], y: Sequence[torch.Tensor], partial_cx: Sequence[torch.Tensor],
+    partial_s: Sequence[torch.Tensor], counters: Sequence[torch.Tensor], coef: Sequence[float],
+    geps: Sequence[float], tau_floor: Sequence[float],
+) -> list[tuple[torch.Tensor, torch.Tensor, torch.Tensor]]:  # fmt: skip
+    """Checks up to eight GEMV outputs in one launch; (passed, rho, tau) per check.
+
+    The native entry of the reference's extension (`bindings.cpp:221-256`): same argument
+    lists, validation order and messages; the launch goes to `pck_blocked_check`.
+    """
+    batch, outputs, device = build_batch(
+        c, a, r, x, y, partial_cx, partial_s, counters, coef, geps, tau_floor
+    )
     with torch.cuda.device(device):
-        err = handle.pck_blocked_check(batch, stream_handle(device))
+        err = lib().pck_blocked_check(batch, stream_handle(device))
     check(err, "checker kernel launch")
     return outputs
+
+
+def batch_for(
+    items: Sequence[tuple[GpuBlockedChecker, torch.Tensor, torch.Tensor]],
+) -> tuple[PckCheckBatch, list[CheckResult], torch.device]:
+    """Launch descriptor and result tensors for up to eight ``(checker, x, y)`` items."""
+    if len({id(checker) for checker, _, _ in items}) != len(items):
+        raise ValueError("each checker may appear only once per call")
+    batch, outputs, device = build_batch(
+        [ch.c for ch, _, _ in items],
+        [ch.a for ch, _, _ in items],
+        [ch.r for ch, _, _ in items],
+        [x for _, x, _ in items],
+        [y for _, _, y in items],
+        [ch._partial_cx for ch, _, _ in items],
+        [ch._partial_s for ch, _, _ in items],
+        [ch._counters for ch, _, _ in items],
+        [ch.coef for ch, _, _ in items],
+        [ch.geps for ch, _, _ in items],
+        [ch.tau_floor for ch, _, _ in items],
+    )
+    return batch, [CheckResult(*out) for out in outputs], device
 
 
 def check_many(

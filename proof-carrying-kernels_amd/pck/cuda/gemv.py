@@ -8,7 +8,9 @@ without synchronising.
 
 from __future__ import annotations
 
+import ctypes
 from collections.abc import Sequence
+from typing import Any
 
 import torch
 
@@ -98,16 +100,9 @@ def gemv_fp8(Q: torch.Tensor, x: torch.Tensor, threads: int = 256) -> torch.Tens
     return _launch("pck_gemv_fp8_coalesced", Q, x, threads, 32, torch.float8_e4m3fn)
 
 
-def gemv_group(
-    pairs: Sequence[tuple[torch.Tensor, torch.Tensor]], threads: int = 256
-) -> list[torch.Tensor]:
-    """Several independent GEMVs of one weight type in one launch (e.g. q, k, v of a layer).
-
-    ``pairs`` holds up to 8 ``(W, x)``; every W is BF16 (coalesced tree) or every W is
-    E4M3FN (the FP8 tree).  Each output has exactly the bits `gemv_coalesced` or `gemv_fp8`
-    would give.  No reference counterpart: the reference fuses such GEMVs by concatenating
-    their weights (`harness/bench_decode_layer.py:48-53`).
-    """
+def _group_descriptors(
+    pairs: Sequence[tuple[torch.Tensor, torch.Tensor]], threads: int
+) -> tuple[ctypes.Array, list[torch.Tensor], int, torch.device]:  # type: ignore[type-arg]
     if not 1 <= len(pairs) <= MAX_GROUP:
         raise RuntimeError(f"group size must be in [1, {MAX_GROUP}], got {len(pairs)}")
     w_type = pairs[0][0].dtype
@@ -125,7 +120,49 @@ def gemv_group(
         y = torch.empty(W.size(0), dtype=torch.float32, device=device)
         descs[g] = PckGemv(W.data_ptr(), x.data_ptr(), y.data_ptr(), W.size(0), W.size(1))
         outs.append(y)
-    kind = 0 if w_type == torch.bfloat16 else 1
+    return descs, outs, (0 if w_type == torch.bfloat16 else 1), device
+
+
+def gemv_group_check(
+    pairs: Sequence[tuple[torch.Tensor, torch.Tensor]],
+    checks: Sequence[tuple[Any, torch.Tensor, torch.Tensor]],
+    threads: int = 256,
+) -> tuple[list[torch.Tensor], list[Any]]:
+    """`gemv_group` plus, in the same launch, the blocked checks of ``checks`` (up to eight
+    ``(GpuBlockedChecker, x, y)`` items whose outputs came from earlier launches on this
+    stream).  Returns the GEMV outputs and one `CheckResult` per check, bit-identical to
+    ``check_many(checks)``.  The checker runs in its own workgroups of the launch and reads y
+    from memory; its latency hides behind the GEMV stream.  No reference counterpart (the
+    reference's checks are always a separate launch)."""
+    from pck.cuda.checker import batch_for
+
+    descs, outs, kind, device = _group_descriptors(pairs, threads)
+    ride = None
+    results: list[Any] = []
+    if checks:
+        ride, results, check_device = batch_for(checks)
+        if check_device != device:
+            raise RuntimeError("the checks must be on the GEMVs' device")
+    with torch.cuda.device(device):
+        err = lib().pck_gemv_group_check(
+            kind, descs, len(pairs), threads, None if ride is None else ctypes.byref(ride),
+            stream_handle(device),
+        )  # fmt: skip
+    check(err, "grouped gemv launch")
+    return outs, results
+
+
+def gemv_group(
+    pairs: Sequence[tuple[torch.Tensor, torch.Tensor]], threads: int = 256
+) -> list[torch.Tensor]:
+    """Several independent GEMVs of one weight type in one launch (e.g. q, k, v of a layer).
+
+    ``pairs`` holds up to 8 ``(W, x)``; every W is BF16 (coalesced tree) or every W is
+    E4M3FN (the FP8 tree).  Each output has exactly the bits `gemv_coalesced` or `gemv_fp8`
+    would give.  No reference counterpart: the reference fuses such GEMVs by concatenating
+    their weights (`harness/bench_decode_layer.py:48-53`).
+    """
+    descs, outs, kind, device = _group_descriptors(pairs, threads)
     with torch.cuda.device(device):
         err = lib().pck_gemv_group(kind, descs, len(pairs), threads, stream_handle(device))
     check(err, "grouped gemv launch")
