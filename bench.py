@@ -2,8 +2,8 @@
 
 A step is one Llama-3-8B decode layer at batch 1 through the hot path: the seven projections
 (q/o 4096x4096, k/v 1024x4096, gate/up 14336x4096, down 4096x14336) as four launches (q, k, v
-grouped; o; gate, up grouped; down), then one launch of the trusted blocked checker over all
-seven outputs at block b = 128, K = 1.  Weights are random (the reference's generator:
+grouped; o; gate, up grouped; down), with all seven outputs checked by the trusted blocked
+checker at block b = 128, K = 1.  Weights are random (the reference's generator:
 N(0, 0.02) BF16, x ~ N(0, 1) BF16) and rotate over several distinct layer copies whose total
 exceeds L2 + MALL, so every step streams its weights from HBM, as decoding through a model does.
 
@@ -11,8 +11,8 @@ A 32-layer decode pass (the depth of Llama-3-8B) cycling over the layer copies i
 in a HIP graph and replayed, as a decode loop replays its captured model (eager Python launches
 leave the GPU idle between kernels; their per-step time is reported beside).  Every GEMV output
 is checked by the trusted blocked checker in a later launch of the same stream: the checker's
-workgroups ride in the next GEMV launch (pck_gemv_group_check; bit-identical to a standalone
-check), so their latency hides behind the weight stream.  The same pass with one standalone
+workgroups ride in a later GEMV launch (pck_gemv_group_check; bit-identical to a standalone
+check), the long gate/up and down launches, so their latency hides behind the weight stream.  The same pass with one standalone
 checker launch per layer (the reference's batched mode) is reported as
 checker_overhead_serial_pct, and with that launch on a side stream as
 checker_overhead_side_stream_pct.
@@ -22,12 +22,15 @@ Printed JSON line:
   roofline       the dominant kernel (the BF16 tree GEMV instance used by q/k/v, o, gate/up):
                  algorithmic bytes per launch / its mean launch duration, from HIP events on
                  the launch stream around a graph that replays those launches back to back
-                 over every layer copy, against 8 TB/s
+                 over every layer copy, against 8 TB/s; traffic = its HBM bytes per launch
+                 from two rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE), as recorded in
+                 the committed summary named by traffic_source
   cpu_baseline   the oracle's CPU model of the same work (coalesced-tree GEMV + CPU blocked
                  checker) timed on this host on a bounded sample
-plus the FP8 layer, GEMV-only times, the checker overhead and a read-only stream ceiling.
+plus the FP8 layer, GEMV-only times, the checker overhead, the membership check (256 x 151936
+logits) and a read-only stream ceiling.
 
-Run: python bench.py [--gpus 1] [--steps 200] [--warmup 20]
+Run: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--quick]
 """
 
 from __future__ import annotations
@@ -44,6 +47,21 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "proof-carrying-kernels_amd"))
 
 HBM_PEAK_GBPS = 8000.0  # MI355X published HBM3E bandwidth
+TRAFFIC_PROFILE = ROOT / "profiles" / "gemv_tree_llama3_8b_decode_layer_hbm_traffic.md"
+
+
+def recorded_traffic() -> int | None:
+    """HBM bytes per launch of the dominant kernel, as recorded from the two counter passes
+    (FETCH_SIZE, WRITE_SIZE, calibrated against a 2 GiB read and fill) in the committed
+    rocprofv3 summary; None if that summary is absent."""
+    try:
+        text = TRAFFIC_PROFILE.read_text()
+    except OSError:
+        return None
+    for line in text.splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1])
+    return None
 LAYER = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
          ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]  # fmt: skip
 LAUNCHES = [("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up")), ("down", ("down",))]
@@ -114,10 +132,16 @@ def run_step(layer, with_check: bool, events=None):  # type: ignore[no-untyped-d
 
 MODE_GEMV, MODE_SERIAL, MODE_OVERLAP, MODE_RIDE = "gemv", "serial", "overlapped", "carried"
 
-# In carried mode each launch of layer L also checks outputs finished by earlier launches:
-# o carries q/k/v's checks, gate_up carries o's, down carries gate/up's, and the next layer's
-# qkv carries down's (the pass ends with one standalone check of the last down).
-CARRIES = {"qkv": ("down",), "o": ("q", "k", "v"), "gate_up": ("o",), "down": ("gate", "up")}
+# In carried mode the long launches of layer L also check outputs finished by earlier launches:
+# gate_up carries the previous layer's down and this layer's q, k, v, o; down carries gate and
+# up; the short q/k/v and o launches carry nothing (the pass ends with one standalone check of
+# the last down).  Each ("prev", name) entry refers to the previous layer's output.
+CARRIES = {
+    "qkv": (),
+    "o": (),
+    "gate_up": (("prev", "down"), ("this", "q"), ("this", "k"), ("this", "v"), ("this", "o")),
+    "down": (("this", "gate"), ("this", "up")),
+}
 
 
 def ride_pass(layers, depth: int):  # type: ignore[no-untyped-def]
@@ -130,14 +154,12 @@ def ride_pass(layers, depth: int):  # type: ignore[no-untyped-def]
         layer = layers[i % len(layers)]
         outs = {}
         for launch, names in LAUNCHES:
-            if launch == "qkv":
-                src = prev
-            else:
-                src = (layer, outs)
             checks = []
-            if src is not None:
-                owner, produced = src
-                checks = [(owner[n][2], owner[n][1], produced[n]) for n in CARRIES[launch]]
+            for which, name in CARRIES[launch]:
+                src = prev if which == "prev" else (layer, outs)
+                if src is not None:
+                    owner, produced = src
+                    checks.append((owner[name][2], owner[name][1], produced[name]))
             ys, res = gemv_group_check([(layer[n][0], layer[n][1]) for n in names], checks, THREADS)
             results.extend(res)
             outs.update(zip(names, ys))
@@ -268,6 +290,86 @@ def timed(layers, steps: int, warmup: int, with_check: bool, per_kernel: bool): 
     return start.elapsed_time(end) / steps, per_launch
 
 
+def membership(copies: int = 4, reps: int = 20) -> dict:
+    """The membership check on BASELINE config 5: 256 x 151,936 FP32 logits ~ N(0, 3) with 8 hot
+    tokens per row at +10..+20, top-k 50, top-p 0.9, 1% of rows given an out-of-set token.  The
+    kernel is launched with prepared arguments over ``copies`` logits buffers (more than the
+    MALL holds), timed with events; the verdicts are checked (planted rows flagged, no false
+    alarm).  GB/s counts the logits read once (155.6 MB per launch)."""
+    import numpy as np
+    import torch
+
+    from pck.cuda._lib import check, lib, stream_handle
+    from pck.fp import next_up
+    from pck.member import member_eps32
+
+    rows, vocab = 256, 151_936
+    g = torch.Generator(device="cuda").manual_seed(0)
+    dev = torch.device("cuda")
+    bufs = []
+    for _ in range(copies):
+        lv = torch.randn(rows, vocab, generator=g, device=dev) * 3
+        hot = torch.randint(0, vocab, (rows, 8), generator=g, device=dev)
+        lv.scatter_add_(1, hot, 10 + 10 * torch.rand(rows, 8, generator=g, device=dev))
+        bufs.append(lv)
+    top = bufs[0].topk(60, dim=1)
+    tokens = top.indices[:, 0].clone()  # the argmax: in every top-k / top-p set
+    planted = torch.zeros(rows, dtype=torch.bool, device=dev)
+    planted[:: rows // (rows // 100)][: rows // 100] = True  # 1% of rows
+    tokens = torch.where(planted, top.indices[:, 55], tokens)  # 55 larger logits: outside top-50
+    k = torch.full((rows,), 50, dtype=torch.long, device=dev)
+    p = torch.full((rows,), 0.9, dtype=torch.float64, device=dev)
+    ok = torch.empty(rows, dtype=torch.bool, device=dev)
+    above = torch.empty(rows, dtype=torch.long, device=dev)
+    mass = torch.empty(rows, dtype=torch.float64, device=dev)
+    slack = next_up(1e-4 + member_eps32(vocab))
+    stream = stream_handle(dev)
+
+    def launch(buf: torch.Tensor) -> None:
+        check(lib().pck_check_members(buf.data_ptr(), rows, vocab, tokens.data_ptr(), k.data_ptr(),
+                                      p.data_ptr(), None, slack, 50, 1, ok.data_ptr(),
+                                      above.data_ptr(), mass.data_ptr(), stream), "members")  # fmt: skip
+
+    launch(bufs[0])
+    torch.cuda.synchronize()
+    flagged = ~ok
+    assert bool((flagged == planted).all()), "membership verdicts differ from the planted faults"
+    for i in range(3):
+        launch(bufs[i % copies])
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(reps):
+        launch(bufs[i % copies])
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / reps
+    nbytes = rows * vocab * 4
+    # CPU baseline: the oracle's FP64 per-row reference on 8 rows, scaled to the same metric
+    from oracle.member import check_member
+
+    host = bufs[0][:8].cpu().numpy()
+    toks = tokens[:8].cpu().numpy()
+    t0 = time.perf_counter()
+    for i in range(8):
+        check_member(host[i], int(toks[i]), 50, 0.9)
+    cpu_s = (time.perf_counter() - t0) / 8 * rows
+    return {
+        "workload": "256 x 151936 fp32 logits, top-k 50, top-p 0.9, 1% planted out-of-set tokens",
+        "ms": round(ms, 5),
+        "gbps": round(nbytes / (ms / 1e3) / 1e9, 1),
+        "pct_of_peak": round(100 * nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 2),
+        "planted_caught": int(planted.sum()),
+        "false_alarms": int((flagged & ~planted).sum()),
+        "cpu_baseline": {
+            "value": round(nbytes / cpu_s / 1e9, 4),
+            "unit": "GB/s",
+            "cores": 1,
+            "kind": "port",
+            "sample": "oracle check_member (FP64, NumPy) on 8 of the 256 rows, scaled to 256",
+        },
+    }
+
+
 def cpu_baseline() -> dict:
     """The oracle on this host: the coalesced-tree CPU model of the q projection (4096 x 4096,
     T = 256) plus the CPU blocked checker at b = 128, K = 1, median of 5 runs; GB/s of the same
@@ -308,7 +410,13 @@ def main() -> None:
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--copies", type=int, default=4, help="distinct layer copies (> MALL)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument(
+        "--quick", action="store_true",
+        help="one pass per mode, no eager timing, no CPU baseline (for counter collection)",
+    )  # fmt: skip
     args = parser.parse_args()
+    if args.quick:
+        args.steps, args.warmup, args.no_cpu_baseline = 32, 1, True
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the decode hot path "
               "here has no multi-GPU step", file=sys.stderr)  # fmt: skip
@@ -343,7 +451,9 @@ def main() -> None:
             assert len(verdicts) == 7 * depth, len(verdicts)
             assert all(bool(r.verdict.all()) for r in verdicts), "checker rejected an honest output"
         del graph, keep
-    ms_eager, per_launch = timed(bf16_layers, args.steps, args.warmup, True, per_kernel=True)
+    ms_eager, per_launch = (float("nan"), {}) if args.quick else timed(
+        bf16_layers, args.steps, args.warmup, True, per_kernel=True
+    )
     dom_ms, dom_bytes = dominant_launch_ms(bf16_layers, max(10, args.steps // 10))
     del bf16_layers
     torch.cuda.empty_cache()
@@ -367,6 +477,8 @@ def main() -> None:
     fp8_checked, fp8_gemv_only = ms8[MODE_RIDE], ms8[MODE_GEMV]
 
     read_ceiling = read_bandwidth_gbps()
+    print("[bench] timing the membership check", file=sys.stderr, flush=True)
+    member = membership()
     achieved = dom_bytes / (dom_ms / 1e3) / 1e9
     value = bytes_bf16 / (ms_checked / 1e3) / 1e9
 
@@ -395,7 +507,7 @@ def main() -> None:
         "checker_overhead_pct": round(100 * (ms_checked / ms_gemv_only - 1), 2),
         "checker_overhead_serial_pct": round(100 * (ms[MODE_SERIAL] / ms_gemv_only - 1), 2),
         "checker_overhead_side_stream_pct": round(100 * (ms[MODE_OVERLAP] / ms_gemv_only - 1), 2),
-        "eager_ms_per_step": round(ms_eager, 5),
+        "eager_ms_per_step": None if args.quick else round(ms_eager, 5),
         "fp8": {
             "value_gbps": round(bytes_fp8 / (fp8_checked / 1e3) / 1e9, 1),
             "gemv_only_gbps": round(bytes_fp8 / (fp8_gemv_only / 1e3) / 1e9, 1),
@@ -408,6 +520,7 @@ def main() -> None:
         },
         "eager_launch_ms": {k: round(statistics.mean(v), 5) for k, v in per_launch.items()},
         "hbm_read_ceiling_gbps": round(read_ceiling, 1),
+        "membership": member,
         "roofline": {
             "bound": "hbm",
             "kernel": "gemv_tree_kernel<256,1,2,bf16,nt> (q/k/v, o, gate/up launches)",
@@ -416,7 +529,8 @@ def main() -> None:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": recorded_traffic(),
+            "traffic_source": TRAFFIC_PROFILE.relative_to(ROOT).as_posix(),
         },
     }
     if not args.no_cpu_baseline:
