@@ -120,7 +120,7 @@ typedef struct PckCheckBatch {
   int32_t count;                    /* 1 .. PCK_MAX_BATCH */
 } PckCheckBatch;
 
-/* One launch checks every described output, one work item (a 512-lane workgroup) per
+/* One launch checks every described output, one work item (a 256-lane workgroup) per
  * (check, block) pair: start[g + 1] - start[g] = checks * num_blocks.  The scratch fields
  * (partial_cx, partial_s, counters) and `segments` keep the reference's descriptor; the
  * kernel reads and writes neither (counters stay zero). */
