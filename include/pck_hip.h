@@ -84,6 +84,20 @@ int pck_gemv_group_check(int weight_kind, const PckGemv* gemvs, int count, int t
 int pck_gemv_set_shape(int rows_per_wave, int unroll, int nontemporal);
 
 /* ---------------------------------------------------------------------------------------------
+ * Batched decode product Y (batch, m) FP32 = X (batch, n) BF16 times W^T, W (m, n) BF16
+ * (weight_kind 0) or E4M3FN codes (weight_kind 1), on the matrix cores.  Each
+ * v_mfma_f32_32x32x16_bf16 carries one 8-column chunk with a zero accumulator, which rounds
+ * RNE_fp32(sum of the 8 exact products, each truncated toward zero to 2^(em - 24),
+ * em = max floor(log2|w|) + floor(log2|x|)).  Chunk results are summed in FP32: 8 K segments
+ * of ceil(ceil(n / 8) / 8) chunks, each from -0.0 in chunk order, then
+ * ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7)).  Tree height 9 + segment + 3.
+ * No reference counterpart on the hot path: the reference's nearest code is the diagnostic
+ * harness/csrc/batched_gemv.cu:25-117 (batch <= 8, FP32 cores).
+ * -------------------------------------------------------------------------------------------*/
+int pck_bgemm(int weight_kind, const void* W, const void* X, float* Y, int64_t m, int64_t n,
+              int64_t batch, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
  * Blocked checksum checker.  Field for field the reference's CheckDesc / CheckBatch
  * (src/pck/cuda/csrc/checker.h:13-44); replaces pck::blocked_check
  * (src/pck/cuda/csrc/checker_kernel.cu:189-196).

@@ -1,0 +1,160 @@
+"""Batched decode product Y = X W^T (B >= 16 path): bit-exact against the oracle's model of the
+kernel's order, within the proven bound of the exact product, and the wrapper's validation."""
+
+from __future__ import annotations
+
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.batched import emulate_batched
+from oracle.gemv import e4m3_values
+from pck.cuda import batched_height, gemm_batched, quantize_fp8
+from pck.fp import bf16, gamma
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _bf16_tensor(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(torch.bfloat16).to(DEV)
+
+
+def _family(rng: np.random.Generator, shape: tuple[int, ...], kind: str) -> np.ndarray:
+    if kind == "real_w":
+        return bf16(rng.standard_normal(shape) * 0.02)
+    if kind == "real_x":
+        return bf16(rng.standard_normal(shape))
+    if kind == "wide":
+        v = (1 + rng.integers(0, 128, shape) / 128.0) * np.exp2(rng.integers(-20, 21, shape))
+        v *= rng.choice([-1.0, 1.0], shape)
+        v[rng.random(shape) < 0.1] = 0
+        return bf16(v)
+    if kind == "cancel":
+        v = rng.choice([-1.0, 1.0], shape) * np.exp2(rng.integers(-4, 13, shape))
+        small = rng.random(shape) < 0.5
+        v[small] = bf16(rng.standard_normal(shape) * 1e-4)[small]
+        return bf16(v)
+    if kind == "tiny":
+        v = (1 + rng.integers(0, 128, shape) / 128.0) * np.exp2(rng.integers(-70, -60, shape))
+        return bf16(v * rng.choice([-1.0, 1.0], shape))
+    raise ValueError(kind)
+
+
+def _run(W: np.ndarray, X: np.ndarray) -> np.ndarray:
+    Y = gemm_batched(_bf16_tensor(W), _bf16_tensor(X))
+    torch.cuda.synchronize()
+    return Y.cpu().numpy()
+
+
+def _same_bits(a: np.ndarray, b: np.ndarray) -> bool:
+    return bool(np.all((a.view(np.uint32) == b.view(np.uint32)) | (np.isnan(a) & np.isnan(b))))
+
+
+SHAPES = [
+    (32, 8, 32),     # one chunk: the raw matrix-core step
+    (64, 64, 16),
+    (33, 24, 7),     # ragged rows, batch below one tile
+    (96, 1000, 40),  # n % 8 != 0: element loads
+    (128, 4096, 128),
+    (64, 512, 256),  # eight batch tiles in one pass
+    (40, 136, 300),  # two batch passes
+    (1, 4104, 1),
+]
+
+
+@pytest.mark.parametrize(("m", "n", "B"), SHAPES)
+@pytest.mark.parametrize("fam", ["real", "wide", "cancel"])
+def test_batched_bits_match_model(m: int, n: int, B: int, fam: str) -> None:
+    rng = np.random.default_rng(m * 7919 + n * 31 + B)
+    W = _family(rng, (m, n), "real_w" if fam == "real" else fam)
+    X = _family(rng, (B, n), "real_x" if fam == "real" else fam)
+    print(f"batched m={m} n={n} B={B} fam={fam}", flush=True)
+    assert _same_bits(_run(W, X), emulate_batched(W, X))
+
+
+@pytest.mark.parametrize(("m", "n", "B"), [(64, 64, 32), (32, 8, 64)])
+def test_batched_tiny_magnitudes_match_model(m: int, n: int, B: int) -> None:
+    """Products in the FP32 subnormal range; the results stay normal here (exactness of a
+    subnormal result is covered by the threshold's floor, not by this model)."""
+    rng = np.random.default_rng(5)
+    W = _family(rng, (m, n), "tiny")
+    X = bf16(rng.standard_normal((B, n)) * 2.0**20)
+    assert _same_bits(_run(W, X), emulate_batched(W, X))
+
+
+@pytest.mark.parametrize(("m", "n", "B"), [(128, 4096, 128), (64, 14336, 16)])
+def test_batched_fp8_bits_match_model(m: int, n: int, B: int) -> None:
+    gen = torch.Generator().manual_seed(m + n + B)
+    Wf = (torch.randn(m, n, generator=gen) * 0.02).to(torch.bfloat16)
+    Q, _ = quantize_fp8(Wf)
+    X = torch.randn(B, n, generator=gen).to(torch.bfloat16)
+    print(f"batched fp8 m={m} n={n} B={B}", flush=True)
+    Y = gemm_batched(Q.to(DEV), X.to(DEV))
+    torch.cuda.synchronize()
+    Qv = e4m3_values()[Q.view(torch.uint8).numpy()].astype(np.float32)
+    assert _same_bits(Y.cpu().numpy(), emulate_batched(Qv, X.float().numpy()))
+
+
+def test_batched_every_fp8_code() -> None:
+    """All 256 E4M3FN codes as weights against a few activations (NaN codes give NaN)."""
+    codes = np.arange(256, dtype=np.uint8).reshape(32, 8)
+    Q = torch.from_numpy(codes).view(torch.float8_e4m3fn)
+    X = bf16(np.random.default_rng(1).standard_normal((16, 8)))
+    Y = gemm_batched(Q.to(DEV), _bf16_tensor(X))
+    torch.cuda.synchronize()
+    Qv = e4m3_values()[codes].astype(np.float32)
+    assert _same_bits(Y.cpu().numpy(), emulate_batched(Qv, X))
+
+
+def test_batched_special_values() -> None:
+    W = np.zeros((32, 16), np.float32)
+    W[0, 0] = np.inf
+    W[1, 0], W[1, 1] = np.inf, -np.inf
+    W[2, 3] = np.nan
+    W[3, :] = bf16(np.float32(3.0e38))
+    W[4:, :] = bf16(np.random.default_rng(2).standard_normal((28, 16)))
+    X = np.ones((16, 16), np.float32)
+    X[5, :] = 2.0
+    assert _same_bits(_run(W, X), emulate_batched(W, X))
+
+
+def test_batched_within_proven_bound() -> None:
+    """|Y - X W^T| <= gamma_h sum |w x| with h = batched_height(n), against exact rationals."""
+    rng = np.random.default_rng(9)
+    m, n, B = 8, 4096, 16
+    W = _family(rng, (m, n), "real_w")
+    X = _family(rng, (B, n), "real_x")
+    Y = _run(W, X)
+    h = batched_height(n)
+    g = gamma(h)
+    for b in range(0, B, 5):
+        for i in range(m):
+            exact = sum(Fraction(float(W[i, j])) * Fraction(float(X[b, j])) for j in range(n))
+            absum = float(np.sum(np.abs(W[i].astype(np.float64) * X[b].astype(np.float64))))
+            assert abs(Fraction(float(Y[b, i])) - exact) <= Fraction(g * absum)
+
+
+def test_batched_height_formula() -> None:
+    assert batched_height(8) == 9 + 1 + 3
+    assert batched_height(4096) == 9 + 64 + 3
+    assert batched_height(14336) == 9 + 224 + 3
+    assert batched_height(4096) == 9 + math.ceil(512 / 8) + 3
+
+
+def test_batched_validation_messages() -> None:
+    W = torch.zeros(4, 8, dtype=torch.bfloat16, device=DEV)
+    X = torch.zeros(2, 8, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="CUDA tensors"):
+        gemm_batched(W.cpu(), X)
+    with pytest.raises(RuntimeError, match="bfloat16"):
+        gemm_batched(W.float(), X)
+    with pytest.raises(RuntimeError, match="shape"):
+        gemm_batched(W, X[:, :4].contiguous())
+    with pytest.raises(RuntimeError, match="contiguous"):
+        gemm_batched(torch.zeros(8, 4, dtype=torch.bfloat16, device=DEV).t(), X)
+    assert gemm_batched(W[:0], X).shape == (2, 0)
