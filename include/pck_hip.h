@@ -143,7 +143,8 @@ int pck_blocked_check(const PckCheckBatch* batch, void* stream);
 /* ---------------------------------------------------------------------------------------------
  * Sampled-token membership check for a batch of rows (top-k / top-p / greedy), the native
  * kernel behind pck.member.check_members (reference src/pck/member.py:118-197).
- *   logits (rows, vocab) FP32; tokens (rows,) int64 (any value: out-of-range ids reject);
+ *   logits (rows, vocab) FP32, 1 <= vocab < 2^31; tokens (rows,) int64 (any value:
+ *   out-of-range ids reject);
  *   top_k (rows,) int64 or NULL (already clamped to [1, vocab]; vocab = no top-k);
  *   top_p (rows,) FP64 or NULL (1 = no top-p); greedy (rows,) uint8 or NULL;
  *   slack = next_up(tol + member_eps32(vocab)) from the host;

@@ -18,14 +18,18 @@
 // verdict is the same (false).
 //
 // Kernel: one workgroup of 1024 lanes per row.
-//   Pass 1 (HBM): count above, NaN flag, row max, and each lane's own maximum.
-//   The k_eff-th largest of the 1024 lane maxima, L0, is a lower bound of kth (k_eff lanes hold
-//   a value >= L0), so every kept logit is >= L0.
-//   Pass 2 (the row is now in L2/MALL): compact the logits >= L0 into LDS (ballot + one LDS
-//   atomic per wave).  For LLM logits that is a few dozen values; kth and both sums then come
-//   from LDS without another pass.  If more than kCap values qualify (flat or adversarial
-//   rows), an exact 4-pass radix select over the row and a summing pass take over.
-//   Rows without a top-k sum over the whole row in pass 2.
+//   Prefix (the first kPrefix logits): count above, NaN flag and each lane's
+//   maximum.  For a top-p row with a top-k, a 16-bit radix select over the 1024 lane maxima
+//   gives L0, a value at or below the k_eff-th largest lane maximum, so at least k_eff logits of
+//   the prefix are >= L0 and L0 is a lower bound of the row's kth (the k-th largest of a part
+//   never exceeds that of the whole).
+//   Stream (the rest of the row, read from HBM once, non-temporal): count above, NaN flag, row
+//   maximum, and the logits >= L0 compacted into LDS (ballot + one LDS atomic per wave); then
+//   the prefix, held in registers (or re-read from L2 for unaligned or short rows), is
+//   compacted too.  For LLM logits that is a few hundred values; kth
+//   and both sums come from LDS with no further pass over the row.  If more than kCap values
+//   qualify (flat or adversarial rows), an exact 4-pass radix select over the row and a summing
+//   pass take over.  Rows without a top-k sum over the whole row in a second pass.
 
 #include <hip/hip_runtime.h>
 
@@ -41,6 +45,7 @@ constexpr int kThreads = 1024;
 constexpr int kWave = 64;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kCap = 4096;  // candidates held in LDS
+constexpr int64_t kPrefix = 16 * kThreads;  // logits that set the candidate threshold
 
 struct MemberArgs {
   const float* logits;
@@ -84,41 +89,43 @@ __device__ __forceinline__ float split_term(float x, float m) {
 struct Scratch {
   float cand[kCap];
   uint32_t lane_key[kThreads];
-  uint32_t hist[256];
+  uint32_t hist[2][256];
   double red_d[2][kWaves];
   int64_t red_i[kWaves];
   float red_f[kWaves];
   int red_flag[kWaves];
   int count;
-  uint32_t digit;
-  int64_t rank;
+  uint32_t digit[2];
+  int64_t rank[2];
 };
 
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
 __device__ __forceinline__ int wave_id() { return static_cast<int>(threadIdx.x) / kWave; }
 
-__device__ int64_t group_sum_i64(int64_t v, Scratch& s) {
+// Workgroup sum of `count`, OR of `flag` and max of `v` in one exchange (two barriers).
+__device__ void group_reduce(int64_t& count, int& flag, float& v, Scratch& s) {
 #pragma unroll
-  for (int off = kWave / 2; off > 0; off /= 2) v += __shfl_xor(v, off, kWave);
-  if (lane_id() == 0) s.red_i[wave_id()] = v;
+  for (int off = kWave / 2; off > 0; off /= 2) {
+    count += __shfl_xor(count, off, kWave);
+    flag |= __shfl_xor(flag, off, kWave);
+    v = fmaxf(v, __shfl_xor(v, off, kWave));
+  }
+  if (lane_id() == 0) {
+    s.red_i[wave_id()] = count;
+    s.red_flag[wave_id()] = flag;
+    s.red_f[wave_id()] = v;
+  }
   __syncthreads();
-  int64_t total = 0;
+  count = 0;
+  flag = 0;
+  v = -__builtin_inff();
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) total += s.red_i[w];
+  for (int w = 0; w < kWaves; ++w) {
+    count += s.red_i[w];
+    flag |= s.red_flag[w];
+    v = fmaxf(v, s.red_f[w]);
+  }
   __syncthreads();
-  return total;
-}
-
-__device__ float group_max(float v, Scratch& s) {
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off /= 2) v = fmaxf(v, __shfl_xor(v, off, kWave));
-  if (lane_id() == 0) s.red_f[wave_id()] = v;
-  __syncthreads();
-  float total = -__builtin_inff();
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) total = fmaxf(total, s.red_f[w]);
-  __syncthreads();
-  return total;
 }
 
 // Two FP64 sums at once (the kept mass and the mass above the token).
@@ -143,73 +150,143 @@ __device__ void group_sum2(double& a, double& b, Scratch& s) {
   __syncthreads();
 }
 
-// Calls f(value) for every logit of the row, each exactly once; float4 loads when aligned.
-template <typename F>
-__device__ __forceinline__ void for_each(const float* __restrict__ row, int64_t vocab, F&& f) {
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <bool kNt>
+__device__ __forceinline__ f32x4 load_quad(const f32x4* p) {
+  if constexpr (kNt) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+
+// Calls f4(quad) for the 16-byte quads and f1(value) for the remaining logits of row[begin,
+// end), each logit exactly once (begin % 4 == 0); four quads in flight per lane when the row is
+// aligned, element loads otherwise.  kNt: non-temporal loads (data read once that need not stay
+// in the caches).  pre() runs once, by every lane, after the first quads are requested and
+// before any is used, so workgroup-wide work placed there overlaps their latency.
+template <bool kNt, typename F4, typename F1, typename P>
+__device__ __forceinline__ void for_each4(const float* __restrict__ row, int64_t begin,
+                                          int64_t end, F4&& f4, F1&& f1, P&& pre) {
   const int t = static_cast<int>(threadIdx.x);
-  int64_t done = 0;
+  int64_t done = begin;
   if ((reinterpret_cast<uintptr_t>(row) & 15) == 0) {
-    const float4* quads = reinterpret_cast<const float4*>(row);
-    const int64_t nq = vocab / 4;
-    int64_t q = t;
-    for (; q + 3 * kThreads < nq; q += 4 * kThreads) {
-      const float4 a = quads[q];
-      const float4 b = quads[q + kThreads];
-      const float4 c = quads[q + 2 * kThreads];
-      const float4 d = quads[q + 3 * kThreads];
-      f(a.x), f(a.y), f(a.z), f(a.w);
-      f(b.x), f(b.y), f(b.z), f(b.w);
-      f(c.x), f(c.y), f(c.z), f(c.w);
-      f(d.x), f(d.y), f(d.z), f(d.w);
+    const f32x4* quads = reinterpret_cast<const f32x4*>(row);
+    const int64_t q1 = end / 4;
+    int64_t q = begin / 4 + t;
+    const bool first = q + 3 * kThreads < q1;
+    f32x4 a, b, c, d;
+    if (first) {
+      a = load_quad<kNt>(quads + q);
+      b = load_quad<kNt>(quads + q + kThreads);
+      c = load_quad<kNt>(quads + q + 2 * kThreads);
+      d = load_quad<kNt>(quads + q + 3 * kThreads);
     }
-    for (; q < nq; q += kThreads) {
-      const float4 a = quads[q];
-      f(a.x), f(a.y), f(a.z), f(a.w);
+    pre();
+    if (first) {
+      f4(a), f4(b), f4(c), f4(d);
+      q += 4 * kThreads;
     }
-    done = nq * 4;
+    for (; q + 3 * kThreads < q1; q += 4 * kThreads) {
+      a = load_quad<kNt>(quads + q);
+      b = load_quad<kNt>(quads + q + kThreads);
+      c = load_quad<kNt>(quads + q + 2 * kThreads);
+      d = load_quad<kNt>(quads + q + 3 * kThreads);
+      f4(a), f4(b), f4(c), f4(d);
+    }
+    for (; q < q1; q += kThreads) f4(load_quad<kNt>(quads + q));
+    done = end > begin ? (q1 * 4 > begin ? q1 * 4 : begin) : end;
+  } else {
+    pre();
   }
-  for (int64_t i = done + t; i < vocab; i += kThreads) f(row[i]);
+  for (int64_t i = done + t; i < end; i += kThreads) f1(row[i]);
+}
+
+template <bool kNt, typename F4, typename F1>
+__device__ __forceinline__ void for_each4(const float* __restrict__ row, int64_t begin,
+                                          int64_t end, F4&& f4, F1&& f1) {
+  for_each4<kNt>(row, begin, end, f4, f1, [] {});
+}
+
+// Calls f(value) for every logit of row[begin, end), each exactly once (begin % 4 == 0).
+template <bool kNt, typename F>
+__device__ __forceinline__ void for_each(const float* __restrict__ row, int64_t begin,
+                                         int64_t end, F&& f) {
+  for_each4<kNt>(row, begin, end, [&](const f32x4& v) { f(v[0]), f(v[1]), f(v[2]), f(v[3]); }, f);
+}
+
+// Inclusive prefix sum over the 64 lanes in VALU cross-lane moves: Hillis-Steele steps of
+// 1, 2, 4 and 8 inside each 16-lane row (row_shr, lanes without a source read 0), then each
+// row's total is carried into the next (row_bcast:15 into rows 1 and 3, row_bcast:31 into rows
+// 2 and 3).
+__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
+  const int x = static_cast<int>(v);
+  int a = x + __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);  // row_shr:1
+  a += __builtin_amdgcn_update_dpp(0, a, 0x112, 0xF, 0xF, true);         // row_shr:2
+  a += __builtin_amdgcn_update_dpp(0, a, 0x114, 0xF, 0xF, true);         // row_shr:4
+  a += __builtin_amdgcn_update_dpp(0, a, 0x118, 0xF, 0xF, true);         // row_shr:8
+  a += __builtin_amdgcn_update_dpp(0, a, 0x142, 0xA, 0xF, false);        // row_bcast:15
+  a += __builtin_amdgcn_update_dpp(0, a, 0x143, 0xC, 0xF, false);        // row_bcast:31
+  return static_cast<uint32_t>(a);
 }
 
 // Key of the rank-th largest (1-based) of `count` keys given by key_of(i), by an exact radix
-// select over 8-bit digits with an LDS histogram.  Every lane returns the same key.
-template <typename K>
+// select over 8-bit digits with an LDS histogram.  Every lane returns the same key.  With
+// kRounds < 4 only the top 8 kRounds bits are selected and the rest are zero: the result is
+// the smallest key of the bucket that holds the rank-th largest.
+template <int kRounds = 4, typename K>
 __device__ uint32_t radix_select(int64_t count, int64_t rank, K&& key_of, Scratch& s) {
   const int t = static_cast<int>(threadIdx.x);
   uint32_t prefix = 0;
   uint32_t mask = 0;
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    if (t < 256) s.hist[t] = 0;
-    __syncthreads();
+  // Round r counts into hist[r % 2] and publishes digit[r % 2] / rank[r % 2]; the other
+  // buffer is cleared meanwhile (its last reader finished before the previous barrier), so a
+  // round needs two barriers.
+  if (t < 256) {
+    s.hist[0][t] = 0;
+    s.hist[1][t] = 0;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int round = 0; round < kRounds; ++round) {
+    const int shift = 24 - 8 * round;
+    const int cur = round & 1;
+    if (round > 0 && t < 256) s.hist[cur ^ 1][t] = 0;
     for (int64_t i = t; i < count; i += kThreads) {
       const uint32_t k = key_of(i);
-      if ((k & mask) == prefix) atomicAdd(&s.hist[(k >> shift) & 255u], 1u);
+      const bool hit = (k & mask) == prefix;
+      const uint32_t digit = (k >> shift) & 255u;
+      // Keys bunch into a few buckets (one exponent byte for every candidate): a wave whose
+      // counted lanes share one digit adds them with one atomic instead of serialising them.
+      const uint64_t counted = __ballot(hit);
+      const uint32_t d0 = __shfl(digit, counted ? __builtin_ctzll(counted) : 0, kWave);
+      if (__ballot(hit && digit != d0) == 0) {
+        if (counted != 0 && lane_id() == __builtin_ctzll(counted))
+          atomicAdd(&s.hist[cur][d0], static_cast<uint32_t>(__builtin_popcountll(counted)));
+      } else if (hit) {
+        atomicAdd(&s.hist[cur][digit], 1u);
+      }
     }
     __syncthreads();
     if (wave_id() == 0) {
       // lane l owns digits 255 - 4l ... 252 - 4l (descending); scan lanes in order
+      // counts fit in 32 bits (the host limits vocab to 2^31 - 1)
       const int l = lane_id();
+      const uint32_t want = static_cast<uint32_t>(rank);
       uint32_t h[4];
-      int64_t own = 0;
+      uint32_t own = 0;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        h[q] = s.hist[255 - 4 * l - q];
+        h[q] = s.hist[cur][255 - 4 * l - q];
         own += h[q];
       }
-      int64_t incl = own;
-#pragma unroll
-      for (int off = 1; off < kWave; off *= 2) {
-        const int64_t up = __shfl_up(incl, off, kWave);
-        if (l >= off) incl += up;
-      }
-      const int64_t excl = incl - own;
-      if (excl < rank && rank <= incl) {
-        int64_t cum = excl;
+      const uint32_t incl = wave_inclusive_sum(own);
+      const uint32_t excl = incl - own;
+      if (excl < want && want <= incl) {
+        uint32_t cum = excl;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          if (cum + h[q] >= rank) {
-            s.digit = static_cast<uint32_t>(255 - 4 * l - q);
-            s.rank = rank - cum;
+          if (cum + h[q] >= want) {
+            s.digit[cur] = static_cast<uint32_t>(255 - 4 * l - q);
+            s.rank[cur] = want - cum;
             break;
           }
           cum += h[q];
@@ -217,10 +294,9 @@ __device__ uint32_t radix_select(int64_t count, int64_t rank, K&& key_of, Scratc
       }
     }
     __syncthreads();
-    prefix |= s.digit << shift;
+    prefix |= s.digit[cur] << shift;
     mask |= 255u << shift;
-    rank = s.rank;
-    __syncthreads();
+    rank = s.rank[cur];
   }
   return prefix;
 }
@@ -239,83 +315,128 @@ __global__ void __launch_bounds__(kThreads) member_kernel(const MemberArgs A) {
   const bool greedy = A.greedy ? A.greedy[r] != 0 : false;
   const double p = A.top_p ? A.top_p[r] : 1.0;
 
-  // Pass 1: exact count above the token, NaN flag, row maximum and lane maxima.
+  const bool want_mass = A.top_p != nullptr && p < 1.0;
+  const bool use_kth = A.all_k || (A.k_lim > 0 && k_row < vocab);
+  const int64_t k_eff = k_row < A.k_lim ? k_row : A.k_lim;
+  const bool fused = want_mass && use_kth && k_eff <= kThreads;
+  const int64_t prefix = vocab < kPrefix ? vocab : kPrefix;
+
+  // Exact count above the token, NaN flag and lane maxima over the prefix (kept in L2).
   uint32_t above_lane = 0;
   int nan = 0;
   float lane_max = -__builtin_inff();
-  for_each(row, vocab, [&](float l) {
+  auto scan = [&](float l) {
     above_lane += l > lt;
     nan |= l != l;
     lane_max = fmaxf(lane_max, l);
-  });
-  const int64_t above = group_sum_i64(above_lane, s);
-  const int any_nan = __syncthreads_or(nan);
-  const float m = group_max(lane_max, s);
+  };
+  // An aligned row with a full prefix keeps its prefix quads in registers for the compaction.
+  const bool held = (reinterpret_cast<uintptr_t>(row) & 15) == 0 && prefix == kPrefix;
+  constexpr int kHeld = kPrefix / (4 * kThreads);
+  f32x4 pq[kHeld];
+  if (held) {
+    const f32x4* quads = reinterpret_cast<const f32x4*>(row);
+#pragma unroll
+    for (int j = 0; j < kHeld; ++j) pq[j] = quads[t + j * kThreads];
+#pragma unroll
+    for (int j = 0; j < kHeld; ++j) scan(pq[j][0]), scan(pq[j][1]), scan(pq[j][2]), scan(pq[j][3]);
+  } else {
+    for_each<false>(row, 0, prefix, scan);
+  }
+
+  // Candidate threshold: the smallest value of the 16-bit key bucket that holds the k_eff-th
+  // largest lane maximum of the prefix (a NaN bit pattern there means -inf: keep everything).
+  // It is selected while the stream's first loads are in flight.
+  float low = -__builtin_inff();
+  auto threshold = [&] {
+    s.lane_key[t] = order_key(lane_max);
+    if (t == 0) s.count = 0;
+    __syncthreads();
+    low = key_value(radix_select<2>(kThreads, k_eff, [&](int64_t i) { return s.lane_key[i]; }, s));
+    if (low != low) low = -__builtin_inff();
+  };
+  // Compacts every logit >= low into LDS (lanes may diverge at the end of a range).
+  auto compact = [&](float l) {
+    const bool take = l >= low;
+    const uint64_t want = __ballot(take);
+    if (want != 0) {
+      const uint64_t active = __ballot(1);
+      const int leader = __builtin_ctzll(active);
+      int base = 0;
+      if (lane_id() == leader) base = atomicAdd(&s.count, __builtin_popcountll(want));
+      base = __shfl(base, leader, kWave);
+      if (take) {
+        const uint64_t below = lane_id() ? want & (~0ull >> (kWave - lane_id())) : 0ull;
+        const int at = base + __builtin_popcountll(below);
+        if (at < kCap) s.cand[at] = l;
+      }
+    }
+  };
+  // Most quads hold no candidate: one ballot per quad decides whether any lane needs compact.
+  auto compact4 = [&](const f32x4& v) {
+    const bool any = (v[0] >= low) | (v[1] >= low) | (v[2] >= low) | (v[3] >= low);
+    if (__ballot(any) != 0) compact(v[0]), compact(v[1]), compact(v[2]), compact(v[3]);
+  };
+  // The rest of the row, streamed from HBM once.
+  if (fused) {
+    for_each4<true>(
+        row, prefix, vocab,
+        [&](const f32x4& v) {
+          scan(v[0]), scan(v[1]), scan(v[2]), scan(v[3]);
+          compact4(v);
+        },
+        [&](float l) {
+          scan(l);
+          compact(l);
+        },
+        threshold);
+    if (held) {
+#pragma unroll
+      for (int j = 0; j < kHeld; ++j) compact4(pq[j]);
+    } else {
+      for_each4<false>(row, 0, prefix, compact4, compact);
+    }
+  } else {
+    for_each<true>(row, prefix, vocab, scan);
+  }
+  int64_t above = above_lane;
+  int any_nan = nan;
+  float m = lane_max;
+  group_reduce(above, any_nan, m, s);
 
   bool ok = !any_nan && in_range && above < (greedy ? 1 : k_row);
   double mass = 0.0;
-  if (A.top_p != nullptr && p < 1.0) {
-    const bool use_kth = A.all_k || (A.k_lim > 0 && k_row < vocab);
+  if (want_mass) {
     double z = 0.0;
     double a = 0.0;
     if (!use_kth) {
-      for_each(row, vocab, [&](float l) {
+      for_each<false>(row, 0, vocab, [&](float l) {
         const float e = split_term(l, m);
         z += e;
         a += l > lt ? e : 0.0;
       });
-    } else {
-      const int64_t k_eff = k_row < A.k_lim ? k_row : A.k_lim;
-      bool in_lds = false;
-      if (k_eff <= kThreads) {
-        s.lane_key[t] = order_key(lane_max);
-        if (t == 0) s.count = 0;
-        __syncthreads();
-        const float low =
-            key_value(radix_select(kThreads, k_eff, [&](int64_t i) { return s.lane_key[i]; }, s));
-        // Pass 2: compact every logit >= low into LDS.
-        for_each(row, vocab, [&](float l) {
-          const bool take = l >= low;
-          const uint64_t want = __ballot(take);
-          if (want != 0) {
-            const uint64_t active = __ballot(1);
-            const int leader = __builtin_ctzll(active);
-            int base = 0;
-            if (lane_id() == leader) base = atomicAdd(&s.count, __builtin_popcountll(want));
-            base = __shfl(base, leader, kWave);
-            if (take) {
-              const uint64_t below = lane_id() ? want & (~0ull >> (kWave - lane_id())) : 0ull;
-              const int at = base + __builtin_popcountll(below);
-              if (at < kCap) s.cand[at] = l;
-            }
-          }
-        });
-        __syncthreads();
-        in_lds = s.count <= kCap;
-      }
-      if (in_lds) {
-        const int64_t count = s.count;
-        const float kth = key_value(
-            radix_select(count, k_eff, [&](int64_t i) { return order_key(s.cand[i]); }, s));
-        for (int64_t i = t; i < count; i += kThreads) {
-          const float l = s.cand[i];
-          if (l >= kth) {
-            const float e = split_term(l, m);
-            z += e;
-            a += l > lt ? e : 0.0;
-          }
+    } else if (fused && s.count <= kCap) {
+      const int64_t count = s.count;
+      const float kth = key_value(
+          radix_select(count, k_eff, [&](int64_t i) { return order_key(s.cand[i]); }, s));
+      for (int64_t i = t; i < count; i += kThreads) {
+        const float l = s.cand[i];
+        if (l >= kth) {
+          const float e = split_term(l, m);
+          z += e;
+          a += l > lt ? e : 0.0;
         }
-      } else {
-        const float kth = key_value(
-            radix_select(vocab, k_eff, [&](int64_t i) { return order_key(row[i]); }, s));
-        for_each(row, vocab, [&](float l) {
-          if (l >= kth) {
-            const float e = split_term(l, m);
-            z += e;
-            a += l > lt ? e : 0.0;
-          }
-        });
       }
+    } else {
+      const float kth = key_value(
+          radix_select(vocab, k_eff, [&](int64_t i) { return order_key(row[i]); }, s));
+      for_each<false>(row, 0, vocab, [&](float l) {
+        if (l >= kth) {
+          const float e = split_term(l, m);
+          z += e;
+          a += l > lt ? e : 0.0;
+        }
+      });
     }
     group_sum2(z, a, s);
     const double ratio = a / z;
@@ -337,7 +458,8 @@ extern "C" int pck_check_members(const float* logits, int64_t rows, int64_t voca
                                  const int64_t* tokens, const int64_t* top_k, const double* top_p,
                                  const uint8_t* greedy, double slack, int64_t k_lim, int all_k,
                                  uint8_t* ok, int64_t* above, double* mass_above, void* stream) {
-  if (rows < 0 || rows * pck::kThreads > 0xFFFFFFFFll || vocab < 1 || k_lim < 0 || k_lim > vocab)
+  if (rows < 0 || rows * pck::kThreads > 0xFFFFFFFFll || vocab < 1 || vocab > 0x7FFFFFFF ||
+      k_lim < 0 || k_lim > vocab)
     return hipErrorInvalidValue;
   if (rows == 0) return hipSuccess;
   if (!logits || !tokens || !ok || !above || !mass_above) return hipErrorInvalidValue;
