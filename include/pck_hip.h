@@ -97,6 +97,25 @@ int pck_gemv_set_shape(int rows_per_wave, int unroll, int nontemporal);
 int pck_bgemm(int weight_kind, const void* W, const void* X, float* Y, int64_t m, int64_t n,
               int64_t batch, void* stream);
 
+/* The same product on operands packed into 32-row tiles, the layout the matrix cores read with
+ * one 16-byte load per lane (8 for E4M3FN weights) per two K-steps: step pair p of tile
+ * `tile`, lane L = 32 h + l holds row 32 tile + l, columns 16p + 4h .. + 3 then
+ * 16p + 8 + 4h .. + 3, at byte ((tile * n / 16 + p) * 64 + L) * Q (Q = 16 for BF16, 8 for
+ * E4M3FN); rows past the end are zero.  pck_bgemm_pack writes that layout from (rows, n)
+ * row-major (kind 0: BF16, kind 1: E4M3FN; dst holds ceil(rows / 32) * 32 * n elements);
+ * weights are packed once at load time, activations per call.  pck_bgemm_packed needs
+ * n % 128 == 0, m % 4 == 0 and 16-byte aligned Wp, Xp and Y, and gives the same bits as
+ * pck_bgemm.  No reference counterpart. */
+int pck_bgemm_pack(int kind, const void* src, void* dst, int64_t rows, int64_t n, void* stream);
+int pck_bgemm_packed(int weight_kind, const void* Wp, const void* Xp, float* Y, int64_t m,
+                     int64_t n, int64_t batch, void* stream);
+
+/* Tuning knob of pck_bgemm_packed: 32-row weight tiles and 32-row batch tiles per workgroup,
+ * (1, 1), (1, 2), (1, 4) or (2, 2); (0, 0) restores the built-in choice.
+ * Changes only speed: outputs keep the same bits.  Process-wide and not thread-safe; no
+ * reference counterpart. */
+int pck_bgemm_set_shape(int rows, int tiles);
+
 /* ---------------------------------------------------------------------------------------------
  * Blocked checksum checker.  Field for field the reference's CheckDesc / CheckBatch
  * (src/pck/cuda/csrc/checker.h:13-44); replaces pck::blocked_check

@@ -21,16 +21,23 @@
 //
 // One step loses at most gamma_9 sum|p|, so an output's tree height is 9 + P + 3.
 //
-// Work decomposition: a workgroup of 8 waves owns 32 weight rows and up to 256 batch rows
-// (eight 32-column MFMA tiles).  Every wave streams the same 32 weight rows over its own K
-// segment, so each weight byte is read from HBM once.  The eight wave sums meet in LDS and
-// leave as coalesced 128-byte rows of Y.  FP8 (E4M3FN) weights are decoded to BF16 in
-// registers; every E4M3 value is exactly a BF16 value, so the products and the model are the
-// same.
+// Work decomposition.  A workgroup of 8 waves owns 32 weight rows and 32 T batch rows (T
+// tiles of 32); wave w owns K segment w for all of them, so each MFMA tile of the workgroup is
+// summed by eight waves and the eight segment sums meet in LDS in the tree order above.
+//   Packed kernel (pck_bgemm_packed): weights and activations in the 32-row tile layout below,
+//   so each load feeds two K-steps of one MFMA operand; rolling register rings keep 16 (8 at
+//   four tiles) K-steps of both operands in flight per lane; the batch passes of one row tile are
+//   dispatched to the same XCD (workgroup g runs on XCD g % 8), so their repeated weight reads
+//   are served by that XCD's L2.
+//   Element kernel (pck_bgemm: any n, any alignment, row-major operands): the same order with
+//   element loads, one K-step at a time.
+// FP8 (E4M3FN) weights are decoded to BF16 in registers; every E4M3 value is exactly a BF16
+// value, so the products and the model are the same.
 
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <utility>
 
 #include "pck_hip.h"
 
@@ -199,6 +206,294 @@ __global__ void __launch_bounds__(kThreads) bgemm_kernel(BgemmArgs a) {
   }
 }
 
+// ---- packed-operand kernel -------------------------------------------------------------------
+//
+// The kernel issues v_mfma_f32_32x32x8_bf16, whose single group of 8 K-slots spans both lane
+// halves (lane l + 32 h holds row / column l, slots 4h .. 4h + 3): the same one-group,
+// zero-accumulator step as above, with every lane carrying operands.  Operands are packed so
+// that one 16-byte load per lane (8 for E4M3 weights) holds the lane's operands of two
+// consecutive steps:
+//   rows in tiles of 32; step pair p = (2p, 2p + 1) of tile `tile`;
+//   lane L = 32 h + l holds row l, columns 16p + 4h .. + 3 then 16p + 8 + 4h .. + 3;
+//   at byte ((tile * C / 2 + p) * 64 + L) * Q,  C = n / 8 steps, Q = 16 (BF16) or 8 (E4M3);
+//   rows past the end are zero.
+// Loads are raw buffer loads: the lane offset is a constant VGPR and the step offset a
+// scalar; batch tiles past the batch read as zero (offsets past num_records).
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr uint32_t kOutOfRange = 0x80000000u;  // a lane offset past every buffer (reads 0)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff), static_cast<int>(soff), 0);
+}
+
+__device__ __forceinline__ u32x4 load8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const auto q = __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(voff),
+                                                      static_cast<int>(soff), 0);
+  return u32x4{static_cast<uint32_t>(q[0]), static_cast<uint32_t>(q[1]), 0u, 0u};
+}
+
+// The lane's four BF16 operands of step j (0 or 1) of a loaded pair.
+template <bool kFp8>
+__device__ __forceinline__ s16x4 w_step(const u32x4& v, int j) {
+  if constexpr (kFp8) {
+    const uint32_t q = j ? v[1] : v[0];
+    return __builtin_bit_cast(s16x4, u32x2{fp8_pair_bf16<false>(q), fp8_pair_bf16<true>(q)});
+  } else {
+    return __builtin_bit_cast(s16x4, j ? u32x2{v[2], v[3]} : u32x2{v[0], v[1]});
+  }
+}
+
+__device__ __forceinline__ s16x4 x_step(const u32x4& v, int j) {
+  return __builtin_bit_cast(s16x4, j ? u32x2{v[2], v[3]} : u32x2{v[0], v[1]});
+}
+
+struct PackedArgs {
+  const char* Wp;  // packed weights, ceil(m / 32) tiles
+  const char* Xp;  // packed activations, ceil(batch / 32) tiles
+  float* Y;        // (batch, m) FP32, row-major, m % 4 == 0, 16-byte aligned
+  int64_t m;
+  int64_t n;
+  int64_t batch;
+  int64_t row_tiles;
+  int64_t batch_tiles;
+  int64_t passes;
+};
+
+// R row tiles (32 weight rows each) and T batch tiles per workgroup: every wave multiplies its
+// K segment of R weight tiles by the same T batch tiles, so each batch load serves R tiles.
+template <int R, int T>
+constexpr int ring_pairs() {
+  return R + T >= 4 ? 4 : 8;
+}
+
+template <int R, int T, bool kFp8>
+__global__ void __launch_bounds__(kThreads) bgemm_packed_kernel(PackedArgs a) {
+  constexpr uint32_t kQ = kFp8 ? 8 : 16;  // weight bytes per lane and step pair
+  // Step pairs in flight per lane, the same for both operands: the vector-memory counter
+  // retires loads in issue order, so a shorter ring for one operand would shorten the other's.
+  constexpr int kRing = ring_pairs<R, T>();
+  // The wave index is uniform: in a scalar register the segment bounds and the loop control
+  // stay scalar, and no load sits under an exec mask (which would make every step wait for
+  // every load in flight).
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / 64);
+  const int lane = static_cast<int>(threadIdx.x) % 64;
+  const int l = lane & 31;
+  const int h = lane >> 5;
+
+  // Workgroup -> (row group, batch pass); the passes of a row group share an XCD.
+  const int64_t g = blockIdx.x;
+  const int64_t groups = (a.row_tiles + R - 1) / R;
+  int64_t rg, bp;
+  if (a.passes > 1 && groups % 8 == 0) {
+    const int64_t xcd = g % 8, local = g / 8;
+    rg = (local / a.passes) * 8 + xcd;
+    bp = local % a.passes;
+  } else {
+    rg = g / a.passes;
+    bp = g % a.passes;
+  }
+  const int64_t rt0 = rg * R;
+  const int64_t rows_here = a.row_tiles - rt0 < R ? a.row_tiles - rt0 : R;
+  // Segments of whole step pairs (the host requires n % 128 == 0, so per is even).
+  const int64_t chunks = a.n / kStep;
+  const int64_t per = (chunks + kWaves - 1) / kWaves;
+  const int64_t c_lo = wave * per < chunks ? wave * per : chunks;
+  const int64_t c_hi = c_lo + per < chunks ? c_lo + per : chunks;
+  const int pairs = static_cast<int>(c_hi - c_lo) / 2;
+
+  // One buffer per operand: this row group of the weights, this pass's batch tiles.
+  const uint32_t w_tile_bytes = static_cast<uint32_t>(chunks / 2 * 64 * kQ);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.Wp + rt0 * w_tile_bytes,
+                                              static_cast<uint32_t>(rows_here) * w_tile_bytes);
+  const int64_t t0 = bp * T;
+  const int64_t tiles_here = a.batch_tiles - t0 < T ? a.batch_tiles - t0 : T;
+  const uint32_t x_tile_bytes = static_cast<uint32_t>(chunks / 2 * 64 * 16);
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(a.Xp + t0 * x_tile_bytes, static_cast<uint32_t>(tiles_here) * x_tile_bytes);
+  uint32_t w_voff[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    w_voff[r] = r < rows_here
+                    ? static_cast<uint32_t>(r * w_tile_bytes + (c_lo / 2 * 64 + lane) * kQ)
+                    : kOutOfRange;
+  }
+  uint32_t x_voff[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    x_voff[t] = t < tiles_here
+                    ? static_cast<uint32_t>(t * x_tile_bytes + (c_lo / 2 * 64 + lane) * 16)
+                    : kOutOfRange;
+  }
+  constexpr uint32_t kWs = 64 * kQ;  // weight bytes per step pair
+  constexpr uint32_t kXs = 64 * 16;  // batch bytes per step pair and tile
+
+  f32x16 acc[R][T];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[r][t][v] = -0.0f;
+  const f32x16 zero16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f,
+                         0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+
+  auto load_w = [&](int r, int pair) {
+    if constexpr (kFp8) return load8(rw, w_voff[r], pair * kWs);
+    else return load16(rw, w_voff[r], pair * kWs);
+  };
+
+  // Rolling register rings: pair q uses slot q % kRing, which is refilled with pair q + kRing
+  // as soon as it is used.  Refills past the segment reload its last pair (unused), so every
+  // load is unconditional and the loads in flight are counted exactly.
+  u32x4 w[kRing][R];
+  u32x4 x[kRing][T];
+  const int last = pairs - 1;
+  if (pairs > 0) {
+#pragma unroll
+    for (int k = 0; k < kRing; ++k) {
+      const int q = k < last ? k : last;
+#pragma unroll
+      for (int r = 0; r < R; ++r) w[k][r] = load_w(r, q);
+#pragma unroll
+      for (int t = 0; t < T; ++t) x[k][t] = load16(rx, x_voff[t], q * kXs);
+    }
+  }
+  // Pair q with ring slot k: two steps of one MFMA per batch tile and 16 adds each, in step
+  // order, then the slot's refill.
+  auto pair_step = [&](int q, auto k_const) {
+    constexpr int k = decltype(k_const)::value;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const s16x4 wv = w_step<kFp8>(w[k][r], j);
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          const f32x16 d = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(wv, x_step(x[k][t], j),
+                                                                   zero16, 0, 0, 0);
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[r][t][v] = acc[r][t][v] + d[v];
+        }
+      }
+    }
+    const int qn = q + kRing < last ? q + kRing : last;
+#pragma unroll
+    for (int r = 0; r < R; ++r) w[k][r] = load_w(r, qn);
+#pragma unroll
+    for (int t = 0; t < T; ++t) x[k][t] = load16(rx, x_voff[t], qn * kXs);
+  };
+  // Whole ring passes have no exit inside, so the loads in flight are the same on every entry
+  // to the loop head and no step waits for more than its own operands.
+  const int full = pairs / kRing * kRing;
+  for (int base = 0; base < full; base += kRing) {
+    [&]<int... K>(std::integer_sequence<int, K...>) {
+      (pair_step(base + K, std::integral_constant<int, K>{}), ...);
+    }(std::make_integer_sequence<int, kRing>{});
+  }
+  // The last partial pass (segments that are not a whole number of passes).
+  [&]<int... K>(std::integer_sequence<int, K...>) {
+    ((full + K < pairs ? (pair_step(full + K, std::integral_constant<int, K>{}), 0) : 0), ...);
+  }(std::make_integer_sequence<int, kRing>{});
+
+  // Segment sums meet in LDS, one row tile at a time:
+  // ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7)).
+  __shared__ float red[4][T][16][64];
+  // r is a compile-time index (a fold over 0 .. R - 1), so acc stays in registers.
+  auto reduce_tile = [&](auto r_const) {
+    constexpr int r = decltype(r_const)::value;
+    auto put = [&](int slot) {
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) red[slot][t][v][lane] = acc[r][t][v];
+    };
+    auto take = [&](int slot) {
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[r][t][v] = acc[r][t][v] + red[slot][t][v][lane];
+    };
+    if constexpr (r > 0) __syncthreads();  // the previous tile's last reads of slot 2
+    if (wave & 1) put(wave / 2);
+    __syncthreads();
+    if (!(wave & 1)) take(wave / 2);  // waves 0, 2, 4, 6 hold s01, s23, s45, s67
+    if (wave == 2) put(1);
+    if (wave == 6) put(3);
+    __syncthreads();
+    if (wave == 0) take(1);  // s0123
+    if (wave == 4) take(3);  // s4567
+    if (wave == 4) put(2);
+    __syncthreads();
+    if (wave == 0) take(2);
+  };
+  [&]<int... Rs>(std::integer_sequence<int, Rs...>) {
+    (reduce_tile(std::integral_constant<int, Rs>{}), ...);
+  }(std::make_integer_sequence<int, R>{});
+  if (wave != 0) return;
+
+  // MFMA output layout: D[i][b] sits in lane b + 32 ((i / 4) % 2), register 4 (i / 8) + i % 4,
+  // so registers 4q .. 4q + 3 of a lane are four consecutive weight rows of one batch row.
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t rt = rt0 + r;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int64_t b = (t0 + t) * 32 + l;
+      if (b >= a.batch) continue;
+      float* yrow = a.Y + b * a.m + rt * kRows + 4 * h;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int64_t i = rt * kRows + 8 * q + 4 * h;
+        if (i < a.m) {
+          *reinterpret_cast<float4*>(yrow + 8 * q) = make_float4(
+              acc[r][t][4 * q], acc[r][t][4 * q + 1], acc[r][t][4 * q + 2], acc[r][t][4 * q + 3]);
+        }
+      }
+    }
+  }
+}
+
+// Packs (rows, n) row-major into the step-pair layout above; kFp8: one byte per element.
+template <bool kFp8>
+__global__ void __launch_bounds__(256) pack_kernel(const char* __restrict__ src,
+                                                   char* __restrict__ dst, int64_t rows,
+                                                   int64_t n, int64_t pieces) {
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (p >= pieces) return;
+  const int64_t pairs = n / (2 * kStep);
+  const int64_t L = p % 64;
+  const int64_t q = (p / 64) % pairs;
+  const int64_t tile = p / (64 * pairs);
+  const int64_t row = tile * 32 + (L & 31);
+  const int64_t col = q * 16 + 4 * (L >> 5);  // first of 4 columns; the second step is +8
+  if constexpr (kFp8) {
+    uint2 v = make_uint2(0u, 0u);
+    if (row < rows) {
+      const char* r = src + row * n;
+      v.x = *reinterpret_cast<const uint32_t*>(r + col);
+      v.y = *reinterpret_cast<const uint32_t*>(r + col + 8);
+    }
+    reinterpret_cast<uint2*>(dst)[p] = v;
+  } else {
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (row < rows) {
+      const char* r = src + row * n * 2;
+      const uint2 lo = *reinterpret_cast<const uint2*>(r + col * 2);
+      const uint2 hi = *reinterpret_cast<const uint2*>(r + (col + 8) * 2);
+      v = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    }
+    reinterpret_cast<uint4*>(dst)[p] = v;
+  }
+}
+
 template <bool kFp8, bool kVector>
 hipError_t launch_tiles(const BgemmArgs& a, int tiles, dim3 grid, hipStream_t stream) {
   switch (tiles) {
@@ -210,6 +505,50 @@ hipError_t launch_tiles(const BgemmArgs& a, int tiles, dim3 grid, hipStream_t st
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+struct PackedShape {
+  int rows;   // row tiles per workgroup (1 or 2)
+  int tiles;  // batch tiles per workgroup (1, 2 or 4)
+};
+
+PackedShape g_shape_override = {0, 0};
+
+// Built-in shape, from a sweep of the Llama-3-8B projections on MI355X: the largest batch tile
+// count that still gives every CU a workgroup (fewer passes over the weights); two weight tiles
+// per workgroup (each batch load serving both) from 256 batch rows on, and at 128 for the
+// middle-sized row counts (q/k/v); four batch tiles only where rows are plentiful.
+PackedShape choose_shape(int64_t row_tiles, int64_t batch) {
+  if (g_shape_override.tiles > 0) return g_shape_override;
+  const int64_t need = (batch + 31) / 32;
+  auto groups = [&](int r, int t) { return (row_tiles + r - 1) / r * ((need + t - 1) / t); };
+  if (need >= 8) return PackedShape{2, 2};
+  if (need >= 4) {
+    if (row_tiles >= 896) return PackedShape{1, 4};
+    if (row_tiles >= 192) return PackedShape{2, 2};
+    return PackedShape{1, 2};
+  }
+  if (need >= 2 && groups(1, 2) >= 256) return PackedShape{1, 2};
+  return PackedShape{1, 1};
+}
+
+template <int R, int T>
+hipError_t launch_rt(PackedArgs a, bool fp8, hipStream_t stream) {
+  a.passes = (a.batch_tiles + T - 1) / T;
+  const int64_t groups = (a.row_tiles + R - 1) / R * a.passes;
+  if (groups > 0x7FFFFFFF / kThreads) return hipErrorInvalidValue;
+  const dim3 grid(static_cast<unsigned>(groups));
+  if (fp8) hipLaunchKernelGGL((bgemm_packed_kernel<R, T, true>), grid, dim3(kThreads), 0, stream, a);
+  else hipLaunchKernelGGL((bgemm_packed_kernel<R, T, false>), grid, dim3(kThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_packed(const PackedArgs& a, PackedShape shape, bool fp8, hipStream_t stream) {
+  if (shape.rows == 2) return shape.tiles == 2 ? launch_rt<2, 2>(a, fp8, stream) : hipErrorInvalidValue;
+  if (shape.tiles == 4) return launch_rt<1, 4>(a, fp8, stream);
+  if (shape.tiles == 2) return launch_rt<1, 2>(a, fp8, stream);
+  if (shape.tiles == 1) return launch_rt<1, 1>(a, fp8, stream);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace
@@ -231,9 +570,58 @@ extern "C" int pck_bgemm(int weight_kind, const void* W, const void* X, float* Y
   const size_t wa = fp8 ? 8 : 16;
   const bool vec = n % kStep == 0 && reinterpret_cast<uintptr_t>(W) % wa == 0 &&
                    reinterpret_cast<uintptr_t>(X) % 16 == 0;
+  auto s = static_cast<hipStream_t>(stream);
   const BgemmArgs a{W, static_cast<const uint16_t*>(X), Y, m, n, batch};
   const dim3 grid(static_cast<unsigned>(row_tiles), static_cast<unsigned>(passes));
-  auto s = static_cast<hipStream_t>(stream);
   if (fp8) return vec ? launch_tiles<true, true>(a, tiles, grid, s) : launch_tiles<true, false>(a, tiles, grid, s);
   return vec ? launch_tiles<false, true>(a, tiles, grid, s) : launch_tiles<false, false>(a, tiles, grid, s);
+}
+
+extern "C" int pck_bgemm_set_shape(int rows, int tiles) {
+  const bool reset = rows == 0 && tiles == 0;
+  const bool valid = (rows == 1 && (tiles == 1 || tiles == 2 || tiles == 4)) ||
+                     (rows == 2 && tiles == 2);
+  if (!reset && !valid) return hipErrorInvalidValue;
+  pck::g_shape_override = pck::PackedShape{rows, tiles};
+  return hipSuccess;
+}
+
+extern "C" int pck_bgemm_pack(int kind, const void* src, void* dst, int64_t rows, int64_t n,
+                              void* stream) {
+  using namespace pck;
+  if ((kind != 0 && kind != 1) || !src || !dst || rows < 1 || n < 128 || n % 128 != 0)
+    return hipErrorInvalidValue;
+  const int64_t tiles = (rows + 31) / 32;
+  const int64_t pieces = tiles * 64 * (n / 16);
+  const int esz = kind == 1 ? 1 : 2;
+  if (tiles * 32 * n * esz > 0xFFFFFFFFll / 2 || reinterpret_cast<uintptr_t>(src) % 8 != 0 ||
+      reinterpret_cast<uintptr_t>(dst) % 16 != 0)
+    return hipErrorInvalidValue;
+  const dim3 grid(static_cast<unsigned>((pieces + 255) / 256));
+  auto s = static_cast<hipStream_t>(stream);
+  if (kind == 1) {
+    hipLaunchKernelGGL((pack_kernel<true>), grid, dim3(256), 0, s, static_cast<const char*>(src),
+                       static_cast<char*>(dst), rows, n, pieces);
+  } else {
+    hipLaunchKernelGGL((pack_kernel<false>), grid, dim3(256), 0, s, static_cast<const char*>(src),
+                       static_cast<char*>(dst), rows, n, pieces);
+  }
+  return hipGetLastError();
+}
+
+extern "C" int pck_bgemm_packed(int weight_kind, const void* Wp, const void* Xp, float* Y,
+                                int64_t m, int64_t n, int64_t batch, void* stream) {
+  using namespace pck;
+  if ((weight_kind != 0 && weight_kind != 1) || !Wp || !Xp || !Y || m < 1 || batch < 1 ||
+      n < 128 || n % 128 != 0 || m % 4 != 0 || reinterpret_cast<uintptr_t>(Y) % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(Wp) % 16 != 0 || reinterpret_cast<uintptr_t>(Xp) % 16 != 0)
+    return hipErrorInvalidValue;
+  const int64_t row_tiles = (m + 31) / 32;
+  const int64_t batch_tiles = (batch + 31) / 32;
+  // One buffer resource covers one weight tile and one pass's batch tiles (32-bit offsets).
+  if ((n / kStep) * 32 * 16 * 4 > 0x7FFFFFFFll) return hipErrorInvalidValue;
+  const PackedArgs a{static_cast<const char*>(Wp), static_cast<const char*>(Xp), Y, m, n, batch,
+                     row_tiles, batch_tiles, 1};
+  return launch_packed(a, choose_shape(row_tiles, batch), weight_kind == 1,
+                       static_cast<hipStream_t>(stream));
 }

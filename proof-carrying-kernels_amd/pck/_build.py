@@ -31,7 +31,7 @@ HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
     "-mcode-object-version=5",
     "-O3",
-    "-std=c++17",
+    "-std=c++20",
     "-fPIC",
     "-ffp-contract=off",
     "-fno-fast-math",

@@ -2,7 +2,7 @@
 the gfx950 library libpck_hip.so.  ``pck.cuda`` keeps the reference's module name: on ROCm,
 PyTorch's device API is ``torch.cuda``."""
 
-from pck.cuda.batched import batched_height, gemm_batched
+from pck.cuda.batched import BatchedWeights, batched_height, gemm_batched, pack_batched_weights
 from pck.cuda.checker import (
     DEFAULT_BLOCK,
     CheckResult,
@@ -27,9 +27,11 @@ __all__ = [
     "GpuBlockedChecker",
     "PendingCheck",
     "SideStreamChecker",
+    "BatchedWeights",
     "batched_height",
     "check_many",
     "gemm_batched",
+    "pack_batched_weights",
     "gemv_coalesced",
     "gemv_fp8",
     "gemv_group",

@@ -73,6 +73,9 @@ SIGNATURES: dict[str, list[Any]] = {
     "pck_gemv_group_check": [_int, ctypes.POINTER(PckGemv), _int, _int, _p, _p],
     "pck_gemv_set_shape": [_int, _int, _int],
     "pck_bgemm": [_int, _p, _p, _p, _i64, _i64, _i64, _p],
+    "pck_bgemm_set_shape": [_int, _int],
+    "pck_bgemm_pack": [_int, _p, _p, _i64, _i64, _p],
+    "pck_bgemm_packed": [_int, _p, _p, _p, _i64, _i64, _i64, _p],
     "pck_blocked_check": [ctypes.POINTER(PckCheckBatch), _p],
     "pck_read_stream": [_p, _i64, _p, _int, _p],
     "pck_check_members": [

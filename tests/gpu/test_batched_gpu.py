@@ -12,7 +12,7 @@ import torch
 
 from oracle.batched import emulate_batched
 from oracle.gemv import e4m3_values
-from pck.cuda import batched_height, gemm_batched, quantize_fp8
+from pck.cuda import batched_height, gemm_batched, pack_batched_weights, quantize_fp8
 from pck.fp import bf16, gamma
 
 pytestmark = pytest.mark.gpu
@@ -45,8 +45,16 @@ def _family(rng: np.random.Generator, shape: tuple[int, ...], kind: str) -> np.n
     raise ValueError(kind)
 
 
-def _run(W: np.ndarray, X: np.ndarray) -> np.ndarray:
-    Y = gemm_batched(_bf16_tensor(W), _bf16_tensor(X))
+def _run(W: np.ndarray, X: np.ndarray, packed: bool = False) -> np.ndarray:
+    Wt = _bf16_tensor(W)
+    Y = gemm_batched(pack_batched_weights(Wt) if packed else Wt, _bf16_tensor(X))
+    torch.cuda.synchronize()
+    return Y.cpu().numpy()
+
+
+def _run_codes(codes: np.ndarray, X: np.ndarray, packed: bool) -> np.ndarray:
+    Q = torch.from_numpy(codes).view(torch.float8_e4m3fn).to(DEV)
+    Y = gemm_batched(pack_batched_weights(Q) if packed else Q, _bf16_tensor(X))
     torch.cuda.synchronize()
     return Y.cpu().numpy()
 
@@ -74,7 +82,39 @@ def test_batched_bits_match_model(m: int, n: int, B: int, fam: str) -> None:
     W = _family(rng, (m, n), "real_w" if fam == "real" else fam)
     X = _family(rng, (B, n), "real_x" if fam == "real" else fam)
     print(f"batched m={m} n={n} B={B} fam={fam}", flush=True)
-    assert _same_bits(_run(W, X), emulate_batched(W, X))
+    want = emulate_batched(W, X)
+    assert _same_bits(_run(W, X), want)
+    assert _same_bits(_run(W, X, packed=True), want)
+
+
+# (m, n, B), all with a packed route (n % 128 == 0, m % 4 == 0): rows past m in the last tile
+# (m = 36, 100), segments of an odd number of step pairs shorter than one ring pass (n = 384:
+# 3 pairs per wave), one ring pass plus a partial one (n = 1152: 9 pairs), several passes
+# (n = 4096), batch tails and several batch passes.
+TILE_SHAPES = [(36, 384, 33), (64, 1152, 100), (32, 4096, 300), (100, 2048, 5)]
+
+
+@pytest.mark.parametrize("shape", [(1, 1), (1, 2), (1, 4), (2, 2)], ids=str)
+@pytest.mark.parametrize(("m", "n", "B"), TILE_SHAPES)
+def test_every_tile_setting_gives_the_model_bits(shape: tuple[int, int], m: int, n: int, B: int) -> None:
+    """Weight and batch tiles per workgroup change only speed: BF16 and FP8 weights, every
+    setting (a last row group with one weight tile when two are asked for: m = 36, 100)."""
+    from pck.cuda._lib import lib
+
+    rng = np.random.default_rng(m + n + B + 10 * shape[0] + shape[1])
+    W = _family(rng, (m, n), "wide")
+    X = _family(rng, (B, n), "real_x")
+    codes = rng.integers(0, 256, (m, n), dtype=np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0  # no NaN codes
+    print(f"batched shape={shape} m={m} n={n} B={B}", flush=True)
+    assert pack_batched_weights(_bf16_tensor(W)).packed is not None
+    try:
+        assert lib().pck_bgemm_set_shape(*shape) == 0
+        assert _same_bits(_run(W, X, packed=True), emulate_batched(W, X))
+        Qv = e4m3_values()[codes].astype(np.float32)
+        assert _same_bits(_run_codes(codes, X, packed=True), emulate_batched(Qv, X))
+    finally:
+        lib().pck_bgemm_set_shape(0, 0)
 
 
 @pytest.mark.parametrize(("m", "n", "B"), [(64, 64, 32), (32, 8, 64)])
@@ -94,10 +134,13 @@ def test_batched_fp8_bits_match_model(m: int, n: int, B: int) -> None:
     Q, _ = quantize_fp8(Wf)
     X = torch.randn(B, n, generator=gen).to(torch.bfloat16)
     print(f"batched fp8 m={m} n={n} B={B}", flush=True)
-    Y = gemm_batched(Q.to(DEV), X.to(DEV))
-    torch.cuda.synchronize()
     Qv = e4m3_values()[Q.view(torch.uint8).numpy()].astype(np.float32)
-    assert _same_bits(Y.cpu().numpy(), emulate_batched(Qv, X.float().numpy()))
+    want = emulate_batched(Qv, X.float().numpy())
+    for packed in (False, True):
+        Wq = pack_batched_weights(Q.to(DEV)) if packed else Q.to(DEV)
+        Y = gemm_batched(Wq, X.to(DEV))
+        torch.cuda.synchronize()
+        assert _same_bits(Y.cpu().numpy(), want)
 
 
 def test_batched_every_fp8_code() -> None:
@@ -158,3 +201,22 @@ def test_batched_validation_messages() -> None:
     with pytest.raises(RuntimeError, match="contiguous"):
         gemm_batched(torch.zeros(8, 4, dtype=torch.bfloat16, device=DEV).t(), X)
     assert gemm_batched(W[:0], X).shape == (2, 0)
+
+
+def test_packed_route_validation_and_fallback() -> None:
+    """Shapes without a packed route (n % 128 != 0, m % 4 != 0) keep the plain weights and give
+    the model's bits through the element kernel; bad arguments raise."""
+    rng = np.random.default_rng(3)
+    for m, n in ((33, 128), (32, 60), (32, 320)):
+        W = _family(rng, (m, n), "real_w")
+        X = _family(rng, (20, n), "real_x")
+        bw = pack_batched_weights(_bf16_tensor(W))
+        assert bw.packed is None and bw.raw is not None
+        assert _same_bits(_run(W, X, packed=True), emulate_batched(W, X))
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        pack_batched_weights(torch.zeros(4, 8, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="BFloat16"):
+        pack_batched_weights(torch.zeros(4, 8, device=DEV))
+    bw = pack_batched_weights(torch.zeros(4, 8, dtype=torch.bfloat16, device=DEV))
+    with pytest.raises(RuntimeError, match="shape"):
+        gemm_batched(bw, torch.zeros(2, 16, dtype=torch.bfloat16, device=DEV))
