@@ -160,6 +160,36 @@ typedef struct PckCheckBatch {
 int pck_blocked_check(const PckCheckBatch* batch, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
+ * Blocked checker for a batch of activation rows (Y = X W^T, B >= 1): every column of Y is
+ * checked as pck_blocked_check checks one GEMV output, against the same bank, signs and
+ * constants (rho = c . X[b] - r . Y[b, beta rows]; tau as for pck_blocked_check with
+ * s = a . |X[b]| bounded above in FP64 and rounded up to FP32).  Outputs (K, nb, batch): index
+ * (k * nb + beta) * batch + b.  One launch checks up to PCK_MAX_BATCH outputs (a whole decode
+ * layer).  The reference checks one vector per descriptor (checker_kernel.cu:87-196); this is
+ * that check for every column, reading the bank once.
+ * -------------------------------------------------------------------------------------------*/
+typedef struct PckBatchCheckDesc {
+  const float* c;      /* (K, nb, n) FP32 checksums r^T W_beta                    */
+  const void* a;       /* (nb, n) BF16 column sums of |W| per block, rounded up   */
+  const int8_t* r;     /* (K, nb, b) secret signs in {-1, +1}                     */
+  const void* X;       /* (batch, n) BF16                                         */
+  const float* Y;      /* (batch, nb * b) FP32 outputs under check                */
+  uint8_t* passed;     /* (K, nb, batch)                                          */
+  double* rho;         /* (K, nb, batch)                                          */
+  double* tau;         /* (K, nb, batch)                                          */
+  int64_t n;           /* columns of W, at most 2^20                              */
+  int64_t block;
+  int64_t num_blocks;
+  int64_t checks;
+  int64_t batch;
+  double coef;
+  double geps;
+  double tau_floor;
+} PckBatchCheckDesc;
+
+int pck_batch_check(const PckBatchCheckDesc* descs, int count, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
  * Sampled-token membership check for a batch of rows (top-k / top-p / greedy), the native
  * kernel behind pck.member.check_members (reference src/pck/member.py:118-197).
  *   logits (rows, vocab) FP32, 1 <= vocab < 2^31; tokens (rows,) int64 (any value:

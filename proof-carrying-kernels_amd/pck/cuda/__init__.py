@@ -9,6 +9,7 @@ from pck.cuda.checker import (
     GpuBlockedChecker,
     PendingCheck,
     SideStreamChecker,
+    check_batched,
     check_many,
     round_up_bf16,
 )
@@ -29,6 +30,7 @@ __all__ = [
     "SideStreamChecker",
     "BatchedWeights",
     "batched_height",
+    "check_batched",
     "check_many",
     "gemm_batched",
     "pack_batched_weights",

@@ -64,6 +64,27 @@ class PckCheckBatch(ctypes.Structure):
     ]
 
 
+class PckBatchCheckDesc(ctypes.Structure):
+    _fields_ = [
+        ("c", _p),
+        ("a", _p),
+        ("r", _p),
+        ("X", _p),
+        ("Y", _p),
+        ("passed", _p),
+        ("rho", _p),
+        ("tau", _p),
+        ("n", _i64),
+        ("block", _i64),
+        ("num_blocks", _i64),
+        ("checks", _i64),
+        ("batch", _i64),
+        ("coef", _f64),
+        ("geps", _f64),
+        ("tau_floor", _f64),
+    ]
+
+
 # name -> (argtypes); every entry point returns int (a hipError_t value)
 SIGNATURES: dict[str, list[Any]] = {
     "pck_gemv_bf16_naive": [_p, _p, _p, _i64, _i64, _int, _p],
@@ -77,6 +98,7 @@ SIGNATURES: dict[str, list[Any]] = {
     "pck_bgemm_pack": [_int, _p, _p, _i64, _i64, _p],
     "pck_bgemm_packed": [_int, _p, _p, _p, _i64, _i64, _i64, _p],
     "pck_blocked_check": [ctypes.POINTER(PckCheckBatch), _p],
+    "pck_batch_check": [ctypes.POINTER(PckBatchCheckDesc), _int, _p],
     "pck_read_stream": [_p, _i64, _p, _int, _p],
     "pck_check_members": [
         _p, _i64, _i64, _p, _p, _p, _p, _f64, _i64, _int, _p, _p, _p, _p,

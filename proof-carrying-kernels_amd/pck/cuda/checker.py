@@ -15,7 +15,15 @@ from dataclasses import dataclass
 
 import torch
 
-from pck.cuda._lib import MAX_BATCH, PckCheckBatch, PckCheckDesc, check, lib, stream_handle
+from pck.cuda._lib import (
+    MAX_BATCH,
+    PckBatchCheckDesc,
+    PckCheckBatch,
+    PckCheckDesc,
+    check,
+    lib,
+    stream_handle,
+)
 from pck.fp import U32, U64, ceil_div, gamma, next_up, sum_up_factor
 
 DEFAULT_BLOCK = 128
@@ -150,6 +158,11 @@ class GpuBlockedChecker:
     def verdict(self, x: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
         """Per-block pass/fail (True = passed every check)."""
         return self.check(x, y).verdict
+
+    def check_batched(self, X: torch.Tensor, Y: torch.Tensor) -> CheckResult:
+        """Check every column of ``Y = X W^T`` (X (B, n) BF16, Y (B, m) FP32); results of
+        shape (checks, num_blocks, B)."""
+        return check_batched([(self, X, Y)])[0]
 
 
 MAX_BATCH_CHECKS = MAX_BATCH
@@ -323,6 +336,54 @@ def check_many(
             [ch.tau_floor for ch, _, _ in chunk],
         )
         results.extend(CheckResult(passed, rho, tau) for passed, rho, tau in outputs)
+    return results
+
+
+def check_batched(
+    items: Sequence[tuple[GpuBlockedChecker, torch.Tensor, torch.Tensor]],
+) -> list[CheckResult]:
+    """Check the outputs of batched products, ``(checker, X, Y)`` each with X (B, n) BF16 and
+    Y (B, m) FP32 (``Y = X W^T``): every column of Y is checked as `check_many` checks one
+    GEMV output, with the checker's bank, signs and constants (build the checker with the
+    height of the batched product's tree).  Up to eight outputs per launch; results have
+    shape (checks, num_blocks, B), and ``verdict`` is then (num_blocks, B).  No reference
+    counterpart: the reference checks one vector per call (`src/pck/cuda/checker.py:143-171`).
+    """
+    results: list[CheckResult] = []
+    for i in range(0, len(items), MAX_BATCH):
+        chunk = items[i : i + MAX_BATCH]
+        descs = (PckBatchCheckDesc * len(chunk))()
+        device = None
+        for g, (ch, X, Y) in enumerate(chunk):
+            if device is None:
+                if not Y.is_cuda:
+                    raise RuntimeError("Y must be a CUDA tensor")
+                device = Y.device
+            _check_tensor(X, "X", torch.bfloat16, device)
+            _check_tensor(Y, "Y", torch.float32, device)
+            if ch.c.device != device:
+                raise RuntimeError(f"the checker's bank must be on {device}")
+            if not (X.dim() == 2 and X.size(1) == ch.n):
+                raise RuntimeError(f"X must have shape (B, {ch.n}), got {list(X.shape)}")
+            if not (Y.dim() == 2 and Y.size(0) == X.size(0) and Y.size(1) == ch.m):
+                raise RuntimeError(f"Y must have shape ({X.size(0)}, {ch.m}), got {list(Y.shape)}")
+            B = X.size(0)
+            shape = (ch.checks, ch.num_blocks, B)
+            passed = torch.empty(shape, dtype=torch.bool, device=device)
+            rho = torch.empty(shape, dtype=torch.float64, device=device)
+            tau = torch.empty(shape, dtype=torch.float64, device=device)
+            results.append(CheckResult(passed, rho, tau))
+            descs[g] = PckBatchCheckDesc(
+                ch.c.data_ptr(), ch.a.data_ptr(), ch.r.data_ptr(), X.data_ptr(), Y.data_ptr(),
+                passed.data_ptr(), rho.data_ptr(), tau.data_ptr(), ch.n, ch.block,
+                ch.num_blocks, ch.checks, B, ch.coef, ch.geps, ch.tau_floor,
+            )  # fmt: skip
+        assert device is not None
+        if any(X.size(0) == 0 for _, X, _ in chunk):
+            raise RuntimeError("batch size must be positive")
+        with torch.cuda.device(device):
+            err = lib().pck_batch_check(descs, len(chunk), stream_handle(device))
+        check(err, "batched checker launch")
     return results
 
 

@@ -1,0 +1,192 @@
+"""The batched blocked checker (every column of Y = X W^T checked) against the oracle: verdicts
+equal to the CPU reference checker, column by column, on the same (W, X[b], Y[b], r) for honest
+and faulty outputs; equal to the single-vector HIP checker; tau within [exact threshold,
+exact (1 + 2^-22)] and rho within its proven rounding; honest batched products at Llama-3-8B
+shapes pass with the batched tree height."""
+
+from __future__ import annotations
+
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+from numpy.typing import NDArray
+
+from oracle.checker import BlockedChecker, WeightBank, gpu_rho_exact, gpu_threshold_exact
+from pck.cuda import (
+    GpuBlockedChecker,
+    batched_height,
+    check_batched,
+    check_many,
+    gemm_batched,
+    pack_batched_weights,
+    quantize_fp8,
+)
+from pck.fp import bf16
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU"),
+]
+
+
+def problem(m: int, n: int, B: int, seed: int):  # type: ignore[no-untyped-def]
+    rng = np.random.default_rng(seed)
+    W = bf16(rng.standard_normal((m, n)) * 0.02)
+    X = bf16(rng.standard_normal((B, n)))
+    Wt = torch.from_numpy(W).to(torch.bfloat16).cuda()
+    Xt = torch.from_numpy(X).to(torch.bfloat16).cuda()
+    return W, X, Wt, Xt
+
+
+def cpu_verdicts(W, X, Y, checker: GpuBlockedChecker, height: int) -> NDArray[np.bool_]:  # type: ignore[no-untyped-def]
+    """(nb, B) verdicts of the CPU reference checker, one column at a time, with the GPU
+    checker's signs."""
+    bank = WeightBank(W, checker.block)
+    signs = checker.r.cpu().numpy().astype(np.float64)
+    cols = []
+    for b in range(X.shape[0]):
+        cpu = BlockedChecker(W, X[b], checker.block, height, bank=bank)
+        cols.append(cpu.verdict_with_signs(Y[b], signs)[0].all(0))
+    return np.stack(cols, axis=1)
+
+
+def faulty(kind: str, Wt: torch.Tensor, Xt: torch.Tensor, rng: np.random.Generator) -> torch.Tensor:
+    """Y with a planted fault: dropped tail columns (the product skips the last four columns
+    of the reduction), BF16 outputs, or one bit flipped per (block, column): the top exponent
+    bit of a random output, or the sign of the block's largest output."""
+    if kind == "legit":
+        return gemm_batched(Wt, Xt)
+    if kind == "skip_tail":
+        Wz = Wt.clone()
+        Wz[:, -4:] = 0
+        return gemm_batched(Wz, Xt)
+    Y = gemm_batched(Wt, Xt)
+    if kind == "bf16_output":
+        return Y.to(torch.bfloat16).float()
+    bit = {"exp_flip": 30, "sign_flip": 31}[kind]
+    y = Y.cpu().numpy().copy()
+    B, m = y.shape
+    if kind == "sign_flip":
+        # the largest output of each block: negating a value below tau / 2 is an error no
+        # rounding bound can separate from rounding (the CPU reference passes it too)
+        rows = np.abs(y).reshape(B, m // 64, 64).argmax(axis=2) + np.arange(0, m, 64)
+    else:
+        rows = rng.integers(0, 64, (B, m // 64)) + np.arange(0, m, 64)
+    bits = y.view(np.uint32)
+    for b in range(B):
+        bits[b, rows[b]] ^= np.uint32(1 << bit)
+    return torch.from_numpy(y).cuda()
+
+
+@pytest.mark.parametrize("kind", ["legit", "skip_tail", "bf16_output", "exp_flip", "sign_flip"])
+def test_verdicts_equal_the_cpu_reference_column_by_column(kind: str) -> None:
+    m, n, B = 256, 1024, 33
+    W, X, Wt, Xt = problem(m, n, B, seed=7)
+    height = batched_height(n)
+    checker = GpuBlockedChecker(Wt, 64, height, checks=3, generator=torch.Generator().manual_seed(7))
+    Y = faulty(kind, Wt, Xt, np.random.default_rng(7))
+    print(f"batch check kind={kind} m={m} n={n} B={B}", flush=True)
+    res = checker.check_batched(Xt, Y)
+    assert res.passed.shape == (3, m // 64, B)
+    gpu = res.verdict.cpu().numpy()
+    np.testing.assert_array_equal(gpu, cpu_verdicts(W, X, Y.cpu().numpy(), checker, height))
+    if kind == "legit":
+        assert gpu.all()
+    elif kind == "bf16_output":
+        assert not gpu.all()  # an error near tau per check: most cells, not every one
+    else:
+        assert not gpu.any()
+
+
+def test_batched_equals_the_single_vector_checker() -> None:
+    """Same bank, same columns: the batched launch and check_many on each column agree on every
+    verdict (the bounds of s differ by at most one FP32 rounding, far from any verdict here)."""
+    m, n, B = 512, 2048, 20
+    _, _, Wt, Xt = problem(m, n, B, seed=8)
+    checker = GpuBlockedChecker(Wt, 128, batched_height(n), checks=2, generator=torch.Generator().manual_seed(8))
+    Y = gemm_batched(Wt, Xt)
+    bad = Y.clone()
+    bad[3, 200] += 1.0
+    bad[17, 5] *= -1.0
+    for out in (Y, bad):
+        res = checker.check_batched(Xt, out)
+        for b in range(B):
+            single = check_many([(checker, Xt[b].contiguous(), out[b].contiguous())])[0]
+            np.testing.assert_array_equal(res.passed[:, :, b].cpu().numpy(), single.passed.cpu().numpy())
+
+
+def test_tau_and_rho_against_exact_arithmetic() -> None:
+    m, n, B = 64, 640, 18
+    _, X, Wt, Xt = problem(m, n, B, seed=9)
+    checker = GpuBlockedChecker(Wt, 32, batched_height(n), checks=2, generator=torch.Generator().manual_seed(9))
+    Y = gemm_batched(Wt, Xt)
+    res = checker.check_batched(Xt, Y)
+    a = checker.a.float().cpu().numpy()
+    c = checker.c.cpu().numpy()
+    r = checker.r.cpu().numpy()
+    tau = res.tau.cpu().numpy()
+    rho = res.rho.cpu().numpy()
+    Yn = Y.cpu().numpy()
+    for b in (0, 7, 17):
+        exact = gpu_threshold_exact(a, X[b], Yn[b], 32, checker.coef, checker.geps, checker.tau_floor)
+        for k in range(2):
+            for beta, te in enumerate(exact):
+                assert Fraction(float(tau[k, beta, b])) >= te
+                assert Fraction(float(tau[k, beta, b])) <= te * (1 + Fraction(1, 2**22))
+        rho_exact = gpu_rho_exact(c, r, X[b], Yn[b])
+        mags = np.abs(c.astype(np.float64)) @ np.abs(X[b].astype(np.float64)) + np.abs(
+            Yn[b].astype(np.float64)
+        ).reshape(-1, 32).sum(1)
+        assert np.all(np.abs(rho[:, :, b] - rho_exact) <= checker.geps * mags * 1.01 + 1e-300)
+
+
+@pytest.mark.parametrize("bad", [math.nan, math.inf])
+def test_non_finite_output_fails_its_block_and_column_only(bad: float) -> None:
+    m, n, B = 256, 512, 40
+    _, _, Wt, Xt = problem(m, n, B, seed=10)
+    checker = GpuBlockedChecker(Wt, 64, batched_height(n), generator=torch.Generator().manual_seed(10))
+    Y = gemm_batched(Wt, Xt)
+    Y[29, 130] = bad
+    expected = np.ones((m // 64, B), dtype=bool)
+    expected[130 // 64, 29] = False
+    np.testing.assert_array_equal(checker.check_batched(Xt, Y).verdict.cpu().numpy(), expected)
+
+
+@pytest.mark.parametrize("B", [128, 256])
+def test_honest_llama_layer_passes(B: int) -> None:
+    """All seven Llama-3-8B projections (q/k/v fused, gate/up fused), packed route, BF16 and
+    FP8 weights, one checker launch for the layer; 0 false alarms."""
+    g = torch.Generator().manual_seed(B)
+    shapes = [(6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336)]
+    for fp8 in (False, True):
+        items = []
+        for m, n in shapes:
+            W = (torch.randn(m, n, generator=g) * 0.02).to(torch.bfloat16).cuda()
+            if fp8:
+                W, _ = quantize_fp8(W)  # the check is against the E4M3 values themselves
+            Wc = W.to(torch.bfloat16)
+            X = torch.randn(B, n, generator=g).to(torch.bfloat16).cuda()
+            Y = gemm_batched(pack_batched_weights(W), X)
+            checker = GpuBlockedChecker(Wc, 128, batched_height(n), generator=torch.Generator().manual_seed(m))
+            items.append((checker, X, Y))
+        print(f"batch check llama B={B} fp8={fp8}", flush=True)
+        for res in check_batched(items):
+            assert bool(res.passed.all())
+            assert bool((res.rho.abs() <= res.tau).all())
+
+
+def test_validation_messages() -> None:
+    _, _, Wt, Xt = problem(128, 256, 4, seed=11)
+    checker = GpuBlockedChecker(Wt, 64, batched_height(256), generator=torch.Generator().manual_seed(11))
+    Y = gemm_batched(Wt, Xt)
+    with pytest.raises(RuntimeError, match="X must be"):
+        checker.check_batched(Xt.float(), Y)
+    with pytest.raises(RuntimeError, match="shape"):
+        checker.check_batched(Xt[:, :128].contiguous(), Y)
+    with pytest.raises(RuntimeError, match="shape"):
+        checker.check_batched(Xt, Y[:3].contiguous())
+    with pytest.raises(RuntimeError, match="CUDA"):
+        checker.check_batched(Xt, Y.cpu())

@@ -55,12 +55,13 @@ LAYOUT_PROGRAM = r"""
 #include "pck_hip.h"
 #define F(T, f) printf(#T "." #f " %zu\n", offsetof(T, f));
 int main(void) {
-  printf("PckGemv %zu\nPckCheckDesc %zu\nPckCheckBatch %zu\n", sizeof(PckGemv),
-         sizeof(PckCheckDesc), sizeof(PckCheckBatch));
+  printf("PckGemv %zu\nPckCheckDesc %zu\nPckCheckBatch %zu\nPckBatchCheckDesc %zu\n",
+         sizeof(PckGemv), sizeof(PckCheckDesc), sizeof(PckCheckBatch), sizeof(PckBatchCheckDesc));
   F(PckGemv, W) F(PckGemv, m) F(PckGemv, n)
   F(PckCheckDesc, tau) F(PckCheckDesc, n) F(PckCheckDesc, seg_len) F(PckCheckDesc, block)
   F(PckCheckDesc, segments) F(PckCheckDesc, coef) F(PckCheckDesc, tau_floor)
   F(PckCheckBatch, start) F(PckCheckBatch, count)
+  F(PckBatchCheckDesc, X) F(PckBatchCheckDesc, n) F(PckBatchCheckDesc, batch) F(PckBatchCheckDesc, tau_floor)
   return 0;
 }
 """
@@ -73,7 +74,8 @@ def test_struct_layouts_match_the_header(tmp_path: Path) -> None:
     subprocess.run(["gcc", "-std=c11", f"-I{HEADER.parent}", str(src), "-o", str(exe)], check=True)
     lines = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
     got = dict(line.rsplit(" ", 1) for line in lines if line)
-    structs = {"PckGemv": _lib.PckGemv, "PckCheckDesc": _lib.PckCheckDesc, "PckCheckBatch": _lib.PckCheckBatch}
+    structs = {"PckGemv": _lib.PckGemv, "PckCheckDesc": _lib.PckCheckDesc, "PckCheckBatch": _lib.PckCheckBatch,
+               "PckBatchCheckDesc": _lib.PckBatchCheckDesc}
     for key, value in got.items():
         if "." in key:
             struct, field = key.split(".")
