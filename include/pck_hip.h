@@ -187,7 +187,13 @@ typedef struct PckBatchCheckDesc {
   double tau_floor;
 } PckBatchCheckDesc;
 
-int pck_batch_check(const PckBatchCheckDesc* descs, int count, void* stream);
+/* Two launches (matrix-core segment partial sums together with the output-side sums; then one
+ * lane per output adding the segments in order) with a caller-allocated workspace of
+ * pck_batch_check_workspace bytes (8-byte aligned); the library allocates nothing.  The
+ * workspace is not shared between calls that overlap.  c 16-byte and a, X 8-byte aligned. */
+int pck_batch_check_workspace(const PckBatchCheckDesc* descs, int count, int64_t* bytes);
+int pck_batch_check(const PckBatchCheckDesc* descs, int count, void* workspace,
+                    int64_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Sampled-token membership check for a batch of rows (top-k / top-p / greedy), the native

@@ -49,6 +49,14 @@ __device__ __forceinline__ double bf16_at(const uint16_t* p, int64_t j) {
   return __uint_as_float(static_cast<uint32_t>(p[j]) << 16);
 }
 
+// Raw buffer resources for the batched checker: a lane offset at or past `bytes` reads zero.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), 0x00020000);
+}
+
 // The smallest FP32 value >= v (v >= 0), widened back to FP64; +inf beyond the FP32 range.
 __device__ __forceinline__ double round_up_to_f32(double v) {
   float f = static_cast<float>(v);

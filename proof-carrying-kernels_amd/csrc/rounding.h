@@ -72,4 +72,14 @@ __device__ __forceinline__ double add_up_nonneg(double a, double b) {
   return err > 0.0 ? raised : s;
 }
 
+// RU(a b) for a, b >= 0 without branches: raised by one ulp when the FMA residual is positive
+// or the product is below 2^-960 (where the residual may be inexact; raising still bounds a b
+// from above); +inf stays +inf (its residual is -inf or NaN) and NaN stays NaN.
+__device__ __forceinline__ double mul_up_nonneg(double a, double b) {
+  const double p = a * b;
+  const double err = __builtin_fma(a, b, -p);
+  const double raised = __longlong_as_double(__double_as_longlong(p) + 1);
+  return (err > 0.0 || p < 0x1p-960) ? raised : p;
+}
+
 }  // namespace pck

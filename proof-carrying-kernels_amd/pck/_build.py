@@ -42,6 +42,11 @@ HIPCC_FLAGS = [
     "-packed-fp32-ops",
 ]
 
+# Per-source additions.  bcheck.hip keeps its matrix-core accumulators in ordinary VGPRs: with
+# the default accumulator-register form the compiler copies every accumulator between register
+# files on each loop pass (measured 6% of the batched checker's time).
+SOURCE_FLAGS = {"bcheck.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 
 def hipcc() -> str:
     found = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
@@ -51,7 +56,8 @@ def hipcc() -> str:
 
 
 def _compile(src: Path, obj: Path) -> None:
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
+    extra = SOURCE_FLAGS.get(src.name, [])
+    cmd = [hipcc(), *HIPCC_FLAGS, *extra, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stderr}")

@@ -98,7 +98,8 @@ SIGNATURES: dict[str, list[Any]] = {
     "pck_bgemm_pack": [_int, _p, _p, _i64, _i64, _p],
     "pck_bgemm_packed": [_int, _p, _p, _p, _i64, _i64, _i64, _p],
     "pck_blocked_check": [ctypes.POINTER(PckCheckBatch), _p],
-    "pck_batch_check": [ctypes.POINTER(PckBatchCheckDesc), _int, _p],
+    "pck_batch_check_workspace": [ctypes.POINTER(PckBatchCheckDesc), _int, ctypes.POINTER(_i64)],
+    "pck_batch_check": [ctypes.POINTER(PckBatchCheckDesc), _int, _p, _i64, _p],
     "pck_read_stream": [_p, _i64, _p, _int, _p],
     "pck_check_members": [
         _p, _i64, _i64, _p, _p, _p, _p, _f64, _i64, _int, _p, _p, _p, _p,

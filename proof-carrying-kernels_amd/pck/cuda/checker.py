@@ -9,6 +9,7 @@ kernel `pck_blocked_check` for up to eight GEMV outputs.
 
 from __future__ import annotations
 
+import ctypes
 import math
 from collections.abc import Sequence
 from dataclasses import dataclass
@@ -349,6 +350,32 @@ def check_batched(
     shape (checks, num_blocks, B), and ``verdict`` is then (num_blocks, B).  No reference
     counterpart: the reference checks one vector per call (`src/pck/cuda/checker.py:143-171`).
     """
+    direct = [item for item in items if _batched_kernel_fits(*item)]
+    out: dict[int, CheckResult] = {}
+    for item in items:
+        if not _batched_kernel_fits(*item):  # one single-vector check per column
+            ch, X, Y = item
+            cols = check_many([(ch, X[b].contiguous(), Y[b].contiguous()) for b in range(X.size(0))])
+            out[id(item)] = CheckResult(
+                torch.stack([r.passed for r in cols], dim=-1),
+                torch.stack([r.rho for r in cols], dim=-1),
+                torch.stack([r.tau for r in cols], dim=-1),
+            )
+    for res, item in zip(_check_batched_direct(direct), direct):
+        out[id(item)] = res
+    return [out[id(item)] for item in items]
+
+
+def _batched_kernel_fits(ch: GpuBlockedChecker, X: torch.Tensor, Y: torch.Tensor) -> bool:
+    """The batched kernel reads eight bank columns and four outputs per load: n % 8 == 0,
+    block % 4 == 0 and 16-byte aligned X and Y (other shapes are checked column by column, with
+    the same verdicts)."""
+    return ch.n % 8 == 0 and ch.block % 4 == 0 and X.data_ptr() % 16 == 0 and Y.data_ptr() % 16 == 0
+
+
+def _check_batched_direct(
+    items: Sequence[tuple[GpuBlockedChecker, torch.Tensor, torch.Tensor]],
+) -> list[CheckResult]:
     results: list[CheckResult] = []
     for i in range(0, len(items), MAX_BATCH):
         chunk = items[i : i + MAX_BATCH]
@@ -381,8 +408,13 @@ def check_batched(
         assert device is not None
         if any(X.size(0) == 0 for _, X, _ in chunk):
             raise RuntimeError("batch size must be positive")
+        need = ctypes.c_int64(0)
+        check(lib().pck_batch_check_workspace(descs, len(chunk), ctypes.byref(need)),
+              "batched checker plan")  # fmt: skip
+        work = torch.empty(max(1, need.value // 8), dtype=torch.float64, device=device)
         with torch.cuda.device(device):
-            err = lib().pck_batch_check(descs, len(chunk), stream_handle(device))
+            err = lib().pck_batch_check(descs, len(chunk), work.data_ptr(), need.value,
+                                        stream_handle(device))  # fmt: skip
         check(err, "batched checker launch")
     return results
 
