@@ -370,6 +370,154 @@ def membership(copies: int = 4, reps: int = 20) -> dict:
     }
 
 
+BATCHED_LAUNCHES = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)]  # fmt: skip
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense BF16 matrix peak
+
+
+def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: int = 2) -> dict:
+    """BASELINE config 4 read literally: a Llama-3-8B decode layer at batch B = 128 and 256 on
+    the matrix cores (four packed launches: q/k/v, o, gate/up, down; BF16 and FP8 weights),
+    every column of every output checked by one batched checker launch per layer (b = 128,
+    K = 1, the batched product's tree height).  32-layer passes over ``copies`` layer copies
+    (more than the MALL holds) are captured in a HIP graph and replayed.  Reported per B and
+    weight type: ms per layer with and without the checker, TFLOP/s (2 B sum(m n) per layer),
+    hipBLASLt's time for the same products (torch.mm, not bit-reproducible) and a fault
+    campaign per kind (BF16 outputs, exponent and sign flips, a dropped reduction tail, BF16
+    partial sums, a BF16 accumulator): planted faults caught and false alarms."""
+    import numpy as np
+    import torch
+
+    from pck.cuda import GpuBlockedChecker, batched_height, check_batched, gemm_batched
+    from pck.cuda import pack_batched_weights, quantize_fp8
+
+    gen = torch.Generator().manual_seed(1)
+    flops_per_row = 2 * sum(m * n for _, m, n in BATCHED_LAUNCHES)
+    raw, layers = [], {False: [], True: []}
+    for _ in range(copies):
+        raw_layer, l16, l8 = [], [], []
+        for _, m, n in BATCHED_LAUNCHES:
+            W = (torch.randn(m, n, generator=gen) * 0.02).to(torch.bfloat16).cuda()
+            Q, _ = quantize_fp8(W)
+            h = batched_height(n)
+            l16.append((pack_batched_weights(W), GpuBlockedChecker(W, BLOCK, h, generator=gen)))
+            l8.append((pack_batched_weights(Q),
+                       GpuBlockedChecker(Q.to(torch.bfloat16), BLOCK, h, generator=gen)))  # fmt: skip
+            raw_layer.append(W)
+        raw.append(raw_layer)
+        layers[False].append(l16)
+        layers[True].append(l8)
+
+    def run_layer(layer, xs, with_check: bool):  # type: ignore[no-untyped-def]
+        ys = [gemm_batched(Wp, X) for (Wp, _), X in zip(layer, xs)]
+        res = check_batched([(ch, X, Y) for (_, ch), X, Y in zip(layer, xs, ys)]) if with_check else None
+        return ys, res
+
+    def time_pass(fn) -> float:  # type: ignore[no-untyped-def]
+        warm = torch.cuda.Stream()
+        warm.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(warm):
+            fn()
+        torch.cuda.current_stream().wait_stream(warm)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / (reps * depth)
+
+    out = {}
+    for B in batches:
+        xs = [torch.randn(B, n, generator=gen).to(torch.bfloat16).cuda() for _, _, n in BATCHED_LAUNCHES]
+        entry = {"batch": B}
+        for fp8 in (False, True):
+            ls = layers[fp8]
+            ys, res = run_layer(ls[0], xs, True)
+            assert all(bool(r.passed.all()) for r in res), "batched checker rejected an honest output"
+            ms_gemm = time_pass(lambda: [run_layer(ls[i % copies], xs, False) for i in range(depth)])
+            ms_chk = time_pass(lambda: [run_layer(ls[i % copies], xs, True) for i in range(depth)])
+            # fault campaign on copy 0: every (block, column) cell of every output, per kind
+            # (reference fault set, harness/numerics_sim.py:58-64 and harness/campaign.py:8-13)
+            rng = np.random.default_rng(B + fp8)
+            kinds: dict[str, list[int]] = {}
+            false_alarms = cells = 0
+
+            def tally(kind: str, v: torch.Tensor) -> None:
+                # v: (num_blocks, B) verdicts; a column (one GEMV output, the reference's unit
+                # in harness/real_activations.py:144-165) is caught if any of its blocks fails
+                c = kinds.setdefault(kind, [0, 0, 0, 0])
+                c[0] += int((~v).sum())
+                c[1] += v.numel()
+                c[2] += int((~v).any(dim=0).sum())
+                c[3] += v.size(1)
+
+            for idx, ((_, ch), X, Y) in enumerate(zip(ls[0], xs, ys)):
+                honest = ch.check_batched(X, Y).verdict
+                false_alarms += int((~honest).sum())
+                cells += honest.numel()
+                m, n = Y.size(1), X.size(1)
+                tally("bf16_output", ch.check_batched(X, Y.to(torch.bfloat16).float()).verdict)
+                for bit, kind in ((30, "exponent_flip"), (31, "sign_flip")):
+                    # top exponent bit of a random output / sign of the block's largest output
+                    y = Y.clone()
+                    blocks = m // BLOCK
+                    if bit == 31:
+                        sel = y.abs().view(B, blocks, BLOCK).argmax(dim=2)
+                    else:
+                        sel = torch.from_numpy(rng.integers(0, BLOCK, (B, blocks))).cuda()
+                    rows = sel + torch.arange(0, m, BLOCK, device=y.device)
+                    bits = y.view(torch.int32)
+                    bits.scatter_(1, rows, bits.gather(1, rows) ^ (1 << bit))
+                    tally(kind, ch.check_batched(X, y).verdict)
+                Wq = quantize_fp8(raw[0][idx])[0] if fp8 else raw[0][idx]
+                Wf = (Wq.float() if not fp8 else Wq.to(torch.float32)).t()  # (n, m)
+                Xf = X.float()
+                # dropped tail: the product skips the last 4 columns of every reduction
+                Wz = Wq.clone()
+                Wz.view(torch.uint8 if fp8 else torch.int16)[:, -4:] = 0
+                tally("skip_tail_4", ch.check_batched(X, gemm_batched(Wz, X)).verdict)
+                # BF16 partials: the 8 K segments' sums rounded to BF16 before they are added
+                seg = -(-n // 8)
+                yp = torch.zeros_like(Y)
+                for j in range(0, n, seg):
+                    yp += (Xf[:, j : j + seg] @ Wf[j : j + seg]).to(torch.bfloat16).float()
+                tally("bf16_partials", ch.check_batched(X, yp).verdict)
+                # BF16 accumulator: the running sum rounded to BF16 after every 32 columns
+                ya = torch.zeros_like(Y)
+                for j in range(0, n, 32):
+                    ya = (ya + Xf[:, j : j + 32] @ Wf[j : j + 32]).to(torch.bfloat16).float()
+                tally("bf16_accumulator", ch.check_batched(X, ya).verdict)
+            planted = sum(c[3] for c in kinds.values())
+            caught = sum(c[2] for c in kinds.values())
+            key = "fp8" if fp8 else "bf16"
+            entry[key] = {
+                "ms_per_layer": round(ms_chk, 5),
+                "gemm_only_ms": round(ms_gemm, 5),
+                "tflops": round(B * flops_per_row / (ms_chk / 1e3) / 1e12, 1),
+                "gemm_only_tflops": round(B * flops_per_row / (ms_gemm / 1e3) / 1e12, 1),
+                "mfma_peak_frac": round(B * flops_per_row / (ms_gemm / 1e3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                "checker_overhead_pct": round(100 * (ms_chk / ms_gemm - 1), 2),
+                "faulty_columns": planted,  # per kind and launch: every column has the fault
+                "faulty_columns_caught": caught,
+                "faults_by_kind": {
+                    k: {"cells_caught": c, "cells": p, "columns_caught": cc, "columns": cp}
+                    for k, (c, p, cc, cp) in kinds.items()
+                },
+                "false_alarms": false_alarms,
+                "honest_cells": cells,
+            }
+        ms_blas = time_pass(lambda: [[torch.mm(X, W.t()) for W, X in zip(raw[i % copies], xs)] for i in range(depth)])
+        entry["hipblaslt_ms_per_layer"] = round(ms_blas, 5)
+        out[f"B{B}"] = entry
+    return out
+
+
 def cpu_baseline(budget_s: float = 10.0) -> dict:
     """The oracle on this host, on one core: the coalesced-tree CPU model of every projection of
     the decode layer (T = 256) plus the CPU blocked checker at b = 128, K = 1, repeated over
@@ -489,6 +637,8 @@ def main() -> None:
     read_ceiling = read_bandwidth_gbps()
     print("[bench] timing the membership check", file=sys.stderr, flush=True)
     member = membership()
+    print("[bench] timing the batched layer (B = 128, 256)", file=sys.stderr, flush=True)
+    batched = batched_layer()
     achieved = dom_bytes / (dom_ms / 1e3) / 1e9
     value = bytes_bf16 / (ms_checked / 1e3) / 1e9
 
@@ -531,6 +681,7 @@ def main() -> None:
         "eager_launch_ms": {k: round(statistics.mean(v), 5) for k, v in per_launch.items()},
         "hbm_read_ceiling_gbps": round(read_ceiling, 1),
         "membership": member,
+        "batched": batched,
         "roofline": {
             "bound": "hbm",
             "kernel": "gemv_tree_kernel<256,1,2,bf16,nt> (q/k/v, o, gate/up launches)",
