@@ -448,6 +448,8 @@ def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: in
             kinds: dict[str, list[int]] = {}
             false_alarms = cells = 0
 
+            by_launch: dict[str, list[int]] = {}
+
             def tally(kind: str, v: torch.Tensor) -> None:
                 # v: (num_blocks, B) verdicts; a column (one GEMV output, the reference's unit
                 # in harness/real_activations.py:144-165) is caught if any of its blocks fails
@@ -456,6 +458,7 @@ def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: in
                 c[1] += v.numel()
                 c[2] += int((~v).any(dim=0).sum())
                 c[3] += v.size(1)
+                by_launch.setdefault(kind, []).append(int((~v).any(dim=0).sum()))
 
             for idx, ((_, ch), X, Y) in enumerate(zip(ls[0], xs, ys)):
                 honest = ch.check_batched(X, Y).verdict
@@ -506,7 +509,8 @@ def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: in
                 "faulty_columns": planted,  # per kind and launch: every column has the fault
                 "faulty_columns_caught": caught,
                 "faults_by_kind": {
-                    k: {"cells_caught": c, "cells": p, "columns_caught": cc, "columns": cp}
+                    k: {"cells_caught": c, "cells": p, "columns_caught": cc, "columns": cp,
+                        "columns_caught_per_launch": dict(zip([x[0] for x in BATCHED_LAUNCHES], by_launch[k]))}
                     for k, (c, p, cc, cp) in kinds.items()
                 },
                 "false_alarms": false_alarms,

@@ -162,8 +162,9 @@ int pck_blocked_check(const PckCheckBatch* batch, void* stream);
 /* ---------------------------------------------------------------------------------------------
  * Blocked checker for a batch of activation rows (Y = X W^T, B >= 1): every column of Y is
  * checked as pck_blocked_check checks one GEMV output, against the same bank, signs and
- * constants (rho = c . X[b] - r . Y[b, beta rows]; tau as for pck_blocked_check with
- * s = a . |X[b]| bounded above in FP64 and rounded up to FP32).  Outputs (K, nb, batch): index
+ * constants (rho = c . X[b] - r . Y[b, beta rows] in FP64; tau as for pck_blocked_check with
+ * s = a . |X[b]| bounded above, at most a factor 1 + 2^-15 over the exact value for
+ * normal-range inputs, and rounded up to FP32).  Outputs (K, nb, batch): index
  * (k * nb + beta) * batch + b.  One launch checks up to PCK_MAX_BATCH outputs (a whole decode
  * layer).  The reference checks one vector per descriptor (checker_kernel.cu:87-196); this is
  * that check for every column, reading the bank once.
@@ -187,10 +188,12 @@ typedef struct PckBatchCheckDesc {
   double tau_floor;
 } PckBatchCheckDesc;
 
-/* Two launches (matrix-core segment partial sums together with the output-side sums; then one
- * lane per output adding the segments in order) with a caller-allocated workspace of
+/* Two launches (matrix-core partial sums per K segment; then a launch that reads the outputs
+ * and adds the segments in a fixed order) with a caller-allocated workspace of
  * pck_batch_check_workspace bytes (8-byte aligned); the library allocates nothing.  The
- * workspace is not shared between calls that overlap.  c 16-byte and a, X 8-byte aligned. */
+ * workspace is not shared between calls that overlap.  Needs n % 8 == 0, block % 4 == 0,
+ * c, a, X, Y 16-byte and r 4-byte aligned, and coef, geps, tau_floor finite and >= 0;
+ * otherwise hipErrorInvalidValue before anything is enqueued. */
 int pck_batch_check_workspace(const PckBatchCheckDesc* descs, int count, int64_t* bytes);
 int pck_batch_check(const PckBatchCheckDesc* descs, int count, void* workspace,
                     int64_t workspace_bytes, void* stream);
