@@ -22,13 +22,15 @@ The reference has no batched kernel on its hot path (its nearest code is the dia
 
 2. The reduction order.  Column chunk c = 8c .. 8c+7 of row i and batch row b gives one step
    result r[b, i, c].  The chunks are dealt to `waves` contiguous segments of
-   ceil(C / waves) chunks, C = ceil(n / 8).  Each segment is summed in FP32 from -0.0 in
-   chunk order, and the segment sums are combined by a neighbour-pair tree
+   P = ceil(C / waves) chunks, C = ceil(n / 8).  Inside a segment, groups of GROUP
+   consecutive chunks (counted from the segment's first chunk) are each summed in FP32 from
+   -0.0 in chunk order, and the group sums are added in group order into the segment sum,
+   from -0.0.  The segment sums are combined by a neighbour-pair tree
    ((s0 + s1) + (s2 + s3)) + ...
 
 Error bound of one step: the truncation loses less than 8 * 2^(em - 24) <= 8 u max|p_k|, and
 the rounding loses u |r|. So |r - sum p| <= gamma_9 sum |p|, and the tree height of an output
-is 9 + (segment length) + log2(waves).
+is 9 + min(P, GROUP) + ceil(P / GROUP) + log2(waves).
 """
 
 from __future__ import annotations
@@ -43,6 +45,9 @@ STEP = 8
 
 WAVES = 8
 """K segments (waves of a workgroup) whose sums the kernel combines."""
+
+GROUP = 16
+"""Chunks per group inside a segment (two-level segment sums)."""
 
 
 def _split(v: NDArray[np.float32]) -> tuple[NDArray[np.int64], NDArray[np.int64], NDArray[np.int64]]:
@@ -122,8 +127,12 @@ def _emulate_rows(W: NDArray[np.float32], X: NDArray[np.float32], waves: int) ->
     sums = []
     for w in range(waves):
         acc = np.full(r.shape[:2], -0.0, np.float32)
-        for c in range(w * per, min(C, (w + 1) * per)):
-            acc = (acc + r[:, :, c]).astype(np.float32)
+        lo, hi = w * per, min(C, (w + 1) * per)
+        for g0 in range(lo, hi, GROUP):
+            grp = np.full(r.shape[:2], -0.0, np.float32)
+            for c in range(g0, min(hi, g0 + GROUP)):
+                grp = (grp + r[:, :, c]).astype(np.float32)
+            acc = (acc + grp).astype(np.float32)
         sums.append(acc)
     while len(sums) > 1:
         sums = [(sums[k] + sums[k + 1]).astype(np.float32) for k in range(0, len(sums), 2)]
@@ -131,7 +140,9 @@ def _emulate_rows(W: NDArray[np.float32], X: NDArray[np.float32], waves: int) ->
 
 
 def batched_height(n: int, waves: int = WAVES) -> int:
-    """Tree height of one output: 9 for the step, the longest segment's additions from -0.0,
-    and log2(waves) for the segment tree."""
+    """Tree height of one output: 9 for the step; for the longest segment of P chunks, at most
+    min(P, GROUP) additions inside a group and ceil(P / GROUP) adding the group sums (each count
+    includes the first addition to -0.0, which is exact); log2(waves) for the segment tree."""
     C = max(1, math.ceil(n / STEP))
-    return 9 + math.ceil(C / waves) + int(math.log2(waves))
+    P = math.ceil(C / waves)
+    return 9 + min(P, GROUP) + math.ceil(P / GROUP) + int(math.log2(waves))

@@ -15,11 +15,14 @@
 // added with ordinary FP32 adds in a fixed order:
 //
 //   chunk c covers columns 8c .. 8c + 7 (columns past n are zero);
-//   wave w of the 8 waves sums chunks [w P, (w + 1) P), P = ceil(ceil(n / 8) / 8), from -0.0
-//     in chunk order;
+//   wave w of the 8 waves owns chunks [w P, (w + 1) P), P = ceil(ceil(n / 8) / 8): groups of
+//     kGroup = 16 consecutive chunks (from the segment's first) are each summed from -0.0 in
+//     chunk order, and the group sums are added in group order into the wave sum, from -0.0;
 //   the eight wave sums combine as ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7)).
 //
-// One step loses at most gamma_9 sum|p|, so an output's tree height is 9 + P + 3.
+// One step loses at most gamma_9 sum|p|, so an output's tree height is
+// 9 + min(P, 16) + ceil(P / 16) + 3: 32 at n = 4096, 42 at n = 14336 (one sequential sum per
+// segment would give 76 and 236, and the checker's threshold grows with the height).
 //
 // Work decomposition.  A workgroup of 8 waves owns 32 weight rows and 32 T batch rows (T
 // tiles of 32); wave w owns K segment w for all of them, so each MFMA tile of the workgroup is
@@ -52,6 +55,7 @@ constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr int kRows = 32;      // weight rows per workgroup
 constexpr int kStep = 8;       // K-slots per populated MFMA group
+constexpr int kGroup = 16;     // chunks per group inside a wave's K segment
 constexpr int kMaxTiles = 8;   // 32-row batch tiles per pass (batch <= 256 per pass)
 constexpr int kLdsTiles = 4;   // tiles combined per LDS round
 
@@ -152,11 +156,11 @@ __global__ void __launch_bounds__(kThreads) bgemm_kernel(BgemmArgs a) {
   const int64_t row = i0 + (lane & 31);
   const bool row_ok = group0 && row < a.m;
 
-  f32x16 acc[kTiles];
+  f32x16 acc[kTiles], grp[kTiles];
 #pragma unroll
   for (int t = 0; t < kTiles; ++t) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) acc[t][v] = -0.0f;
+    for (int v = 0; v < 16; ++v) acc[t][v] = grp[t][v] = -0.0f;
   }
   const f32x16 zero = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f,
                        0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -169,7 +173,17 @@ __global__ void __launch_bounds__(kThreads) bgemm_kernel(BgemmArgs a) {
       const bf16x8 xv = load_x(X, b, a.n, c, group0 && b < batch, kVector);
       const f32x16 d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wv, xv, zero, 0, 0, 0);
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[t][v] = acc[t][v] + d[v];
+      for (int v = 0; v < 16; ++v) grp[t][v] = grp[t][v] + d[v];
+    }
+    if ((c - c_lo) % kGroup == kGroup - 1 || c + 1 == c_hi) {  // the group ends: add it
+#pragma unroll
+      for (int t = 0; t < kTiles; ++t) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          acc[t][v] = acc[t][v] + grp[t][v];
+          grp[t][v] = -0.0f;
+        }
+      }
     }
   }
 
@@ -335,13 +349,27 @@ __global__ void __launch_bounds__(kThreads) bgemm_packed_kernel(PackedArgs a) {
   constexpr uint32_t kWs = 64 * kQ;  // weight bytes per step pair
   constexpr uint32_t kXs = 64 * 16;  // batch bytes per step pair and tile
 
-  f32x16 acc[R][T];
+  f32x16 acc[R][T], grp[R][T];
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[r][t][v] = -0.0f;
+      for (int v = 0; v < 16; ++v) acc[r][t][v] = grp[r][t][v] = -0.0f;
+  // A group of kGroup chunks is kGroup / 2 step pairs; its sum joins the wave sum.
+  constexpr int kGroupPairs = kGroup / 2;
+  static_assert(kGroupPairs % ring_pairs<R, T>() == 0, "groups end at ring pass ends");
+  auto flush = [&]() {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          acc[r][t][v] = acc[r][t][v] + grp[r][t][v];
+          grp[r][t][v] = -0.0f;
+        }
+  };
   const f32x16 zero16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f,
                          0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 
@@ -380,7 +408,7 @@ __global__ void __launch_bounds__(kThreads) bgemm_packed_kernel(PackedArgs a) {
           const f32x16 d = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(wv, x_step(x[k][t], j),
                                                                    zero16, 0, 0, 0);
 #pragma unroll
-          for (int v = 0; v < 16; ++v) acc[r][t][v] = acc[r][t][v] + d[v];
+          for (int v = 0; v < 16; ++v) grp[r][t][v] = grp[r][t][v] + d[v];
         }
       }
     }
@@ -397,11 +425,14 @@ __global__ void __launch_bounds__(kThreads) bgemm_packed_kernel(PackedArgs a) {
     [&]<int... K>(std::integer_sequence<int, K...>) {
       (pair_step(base + K, std::integral_constant<int, K>{}), ...);
     }(std::make_integer_sequence<int, kRing>{});
+    if ((base + kRing) % kGroupPairs == 0) flush();  // uniform
   }
-  // The last partial pass (segments that are not a whole number of passes).
+  // The last partial pass (segments that are not a whole number of passes); it stays inside
+  // one group, which ends with the segment.
   [&]<int... K>(std::integer_sequence<int, K...>) {
     ((full + K < pairs ? (pair_step(full + K, std::integral_constant<int, K>{}), 0) : 0), ...);
   }(std::make_integer_sequence<int, kRing>{});
+  if (pairs % kGroupPairs != 0) flush();
 
   // Segment sums meet in LDS, one row tile at a time:
   // ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7)).
@@ -522,12 +553,12 @@ PackedShape choose_shape(int64_t row_tiles, int64_t batch) {
   if (g_shape_override.tiles > 0) return g_shape_override;
   const int64_t need = (batch + 31) / 32;
   auto groups = [&](int r, int t) { return (row_tiles + r - 1) / r * ((need + t - 1) / t); };
-  if (need >= 8) return PackedShape{2, 2};
-  if (need >= 4) {
-    if (row_tiles >= 896) return PackedShape{1, 4};
-    if (row_tiles >= 192) return PackedShape{2, 2};
-    return PackedShape{1, 2};
-  }
+  // Measured on MI355X at the Llama-3-8B decode shapes (m = 4096 .. 28672, n = 4096, 14336)
+  // with the weights streamed from HBM: at 8 batch tiles, (2, 2) unless it leaves fewer than
+  // 1024 workgroups over more than 128 row tiles; at 4 batch tiles, (2, 2) from 192 row tiles
+  // up, else (1, 2).
+  if (need >= 8) return row_tiles > 128 && groups(2, 2) < 1024 ? PackedShape{1, 1} : PackedShape{2, 2};
+  if (need >= 4) return row_tiles >= 192 ? PackedShape{2, 2} : PackedShape{1, 2};
   if (need >= 2 && groups(1, 2) >= 256) return PackedShape{1, 2};
   return PackedShape{1, 1};
 }

@@ -24,15 +24,18 @@ from pck.cuda._lib import check, lib, stream_handle
 
 STEP = 8
 WAVES = 8
+GROUP = 16  # chunks per group inside a K segment
 TILE = 32
 PAIR_COLUMNS = 128  # packed route: K segments of whole step pairs
 
 
 def batched_height(n: int) -> int:
     """Tree height of one output of `gemm_batched`: 9 for a matrix-core step (8 truncated
-    products, one rounding), the longest K segment's additions, and 3 for the segment tree."""
+    products, one rounding); for the longest K segment of P chunks, min(P, 16) additions inside
+    a group of 16 chunks plus ceil(P / 16) adding the group sums; 3 for the segment tree."""
     chunks = max(1, math.ceil(n / STEP))
-    return 9 + math.ceil(chunks / WAVES) + int(math.log2(WAVES))
+    per = math.ceil(chunks / WAVES)
+    return 9 + min(per, GROUP) + math.ceil(per / GROUP) + int(math.log2(WAVES))
 
 
 @dataclass

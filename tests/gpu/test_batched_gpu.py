@@ -3,13 +3,13 @@ kernel's order, within the proven bound of the exact product, and the wrapper's 
 
 from __future__ import annotations
 
-import math
 from fractions import Fraction
 
 import numpy as np
 import pytest
 import torch
 
+from oracle.batched import batched_height as oracle_height
 from oracle.batched import emulate_batched
 from oracle.gemv import e4m3_values
 from pck.cuda import batched_height, gemm_batched, pack_batched_weights, quantize_fp8
@@ -183,10 +183,11 @@ def test_batched_within_proven_bound() -> None:
 
 
 def test_batched_height_formula() -> None:
-    assert batched_height(8) == 9 + 1 + 3
-    assert batched_height(4096) == 9 + 64 + 3
-    assert batched_height(14336) == 9 + 224 + 3
-    assert batched_height(4096) == 9 + math.ceil(512 / 8) + 3
+    assert batched_height(8) == 9 + 1 + 1 + 3  # one chunk: one group of one
+    assert batched_height(4096) == 9 + 16 + 4 + 3  # 64 chunks per segment: 4 groups of 16
+    assert batched_height(14336) == 9 + 16 + 14 + 3  # 224 chunks per segment
+    for n in range(1, 40000, 97):
+        assert batched_height(n) == oracle_height(n)
 
 
 def test_batched_validation_messages() -> None:
