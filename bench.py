@@ -370,6 +370,48 @@ def membership(copies: int = 4, reps: int = 20) -> dict:
     }
 
 
+SAMPLING_REFERENCE_MS = {  # harness/bench_sampling_out.txt:6-13 (RTX 5060, cold L2, median)
+    "B1": {"topk_checker": 0.0253, "topp_checker": 0.0666},
+    "B8": {"topk_checker": 0.0378, "topp_checker": 0.1649},
+}
+
+
+def sampling_checker(reps: int = 200) -> dict:
+    """The set-sampling checker as the reference's harness/bench_sampling.py times it: V =
+    151,936, k = 50, p = 0.9, logits ~ N(0, 3) at batch 1 and 8, each call timed on a cold L2
+    and MALL (median of ``reps``), the whole Python call included (scratch allocation and the
+    three launches), next to the untrusted samplers it checks.  A selection with one wrong
+    index must fail."""
+    import torch
+
+    from pck.cuda import check_topk_gpu, check_topp_gpu, topk_sample, topp_select
+    from pck.cuda.timing import ColdL2Timer
+
+    vocab, k, p = 151_936, 50, 0.9
+    timer = ColdL2Timer(20, reps)
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    out: dict = {"workload": f"V = {vocab}, top-k {k}, top-p {p}, logits ~ N(0, 3), cold L2 + MALL"}
+    for batch in (1, 8):
+        logits = torch.randn(batch, vocab, generator=gen, device="cuda") * 3
+        selected, _ = topk_sample(logits, k)
+        nucleus, lengths = topp_select(logits, p)
+        assert check_topk_gpu(logits, selected, k).passed.all(), "top-k checker false alarm"
+        assert check_topp_gpu(logits, nucleus, lengths, p, tol=1e-5).passed.all(), "top-p checker false alarm"
+        bad = selected.clone()
+        bad[:, 0] = nucleus[:, -1]  # the smallest logit of each row instead of a top-k one
+        assert not check_topk_gpu(logits, bad, k).passed.any(), "planted top-k fault missed"
+        times = {
+            "topk_checker": timer(lambda: check_topk_gpu(logits, selected, k)),  # noqa: B023
+            "topp_checker": timer(lambda: check_topp_gpu(logits, nucleus, lengths, p)),  # noqa: B023
+            "topk_sampler": timer(lambda: topk_sample(logits, k)),  # noqa: B023
+            "topp_selection": timer(lambda: topp_select(logits, p)),  # noqa: B023
+        }
+        out[f"B{batch}"] = {name: round(t.median_ms, 4) for name, t in times.items()}
+        out[f"B{batch}"]["mean_nucleus"] = round(float(lengths.double().mean()), 1)
+    out["reference_rtx5060_ms"] = SAMPLING_REFERENCE_MS
+    return out
+
+
 BATCHED_LAUNCHES = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)]  # fmt: skip
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense BF16 matrix peak
 
@@ -641,6 +683,8 @@ def main() -> None:
     read_ceiling = read_bandwidth_gbps()
     print("[bench] timing the membership check", file=sys.stderr, flush=True)
     member = membership()
+    print("[bench] timing the set-sampling checker", file=sys.stderr, flush=True)
+    sampling = sampling_checker(50 if args.quick else 200)
     print("[bench] timing the batched layer (B = 128, 256)", file=sys.stderr, flush=True)
     batched = batched_layer()
     achieved = dom_bytes / (dom_ms / 1e3) / 1e9
@@ -685,6 +729,7 @@ def main() -> None:
         "eager_launch_ms": {k: round(statistics.mean(v), 5) for k, v in per_launch.items()},
         "hbm_read_ceiling_gbps": round(read_ceiling, 1),
         "membership": member,
+        "sampling": sampling,
         "batched": batched,
         "roofline": {
             "bound": "hbm",

@@ -214,6 +214,28 @@ int pck_check_members(const float* logits, int64_t rows, int64_t vocab, const in
                       double slack, int64_t k_lim, int all_k, uint8_t* ok, int64_t* above,
                       double* mass_above, void* stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * Set-sampling checker (top-k / top-p): is sel[b, 0 .. len[b]) a valid top-k set (top_p = 0,
+ * length k) or a valid minimal top-p nucleus (top_p = 1) of row b of logits (rows, vocab) FP32?
+ * Replaces pck::sampling_check (reference src/pck/cuda/csrc/sampling_kernel.cu:211-229) with
+ * the same arguments and outputs:
+ *   passed (rows,) uint8; min_selected, max_rejected (rows,) FP32, exact; mass and
+ *   mass_without_smallest (rows,) FP64 (0 unless top-p and the set checks passed).
+ * slack is the host's: the sampler's declared error plus this kernel's own rounding.
+ * scratch: rows * pck_sampling_scratch_words(vocab) uint32, zero on entry (the caller zeroes it;
+ * it holds the selection bitmaps and a malformed flag per row).  partials: rows * segments *
+ * pck_sampling_partial_bytes(), 8-byte aligned.  1 <= segments <= vocab, rows <= 65535,
+ * temperature > 0, slack >= 0.  Three launches: mark, segment, finish.
+ * -------------------------------------------------------------------------------------------*/
+int64_t pck_sampling_scratch_words(int64_t vocab);
+int64_t pck_sampling_partial_bytes(void);
+int pck_sampling_check(const float* logits, const int64_t* selected, const int64_t* lengths,
+                       int64_t rows, int64_t vocab, int64_t max_len, int64_t k, int top_p,
+                       double p, double temperature, double slack, int64_t segments,
+                       uint32_t* scratch, void* partials, uint8_t* passed, float* min_selected,
+                       float* max_rejected, double* mass, double* mass_without_smallest,
+                       void* stream);
+
 /* Measurement: reads `bytes` (a multiple of 16, 16-byte aligned) from `src` with `groups`
  * workgroups of 256 lanes and stores one word per workgroup into sink[groups].  The practical
  * HBM read ceiling for the GEMV roofline; no reference counterpart (the reference measures a

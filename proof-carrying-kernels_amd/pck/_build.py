@@ -24,7 +24,7 @@ ROOT = PACKAGE.parent
 CSRC = ROOT / "csrc"
 INCLUDE = ROOT.parent / "include"
 LIBRARY = PACKAGE / "libpck_hip.so"
-SOURCES = ("gemv.hip", "bgemm.hip", "checker.hip", "bcheck.hip", "member.hip", "measure.hip")
+SOURCES = ("gemv.hip", "bgemm.hip", "checker.hip", "bcheck.hip", "member.hip", "sampling.hip", "measure.hip")
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

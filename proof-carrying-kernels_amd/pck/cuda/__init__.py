@@ -13,6 +13,15 @@ from pck.cuda.checker import (
     check_many,
     round_up_bf16,
 )
+from pck.cuda.sampling import (
+    SamplingCheck,
+    check_topk_gpu,
+    check_topp_gpu,
+    default_segments,
+    sharded_topk_gpu,
+    topk_sample,
+    topp_select,
+)
 from pck.cuda.gemv import (
     gemv_coalesced,
     gemv_fp8,
@@ -41,4 +50,11 @@ __all__ = [
     "gemv_naive",
     "quantize_fp8",
     "round_up_bf16",
+    "SamplingCheck",
+    "check_topk_gpu",
+    "check_topp_gpu",
+    "default_segments",
+    "sharded_topk_gpu",
+    "topk_sample",
+    "topp_select",
 ]

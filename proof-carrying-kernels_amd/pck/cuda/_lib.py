@@ -104,6 +104,15 @@ SIGNATURES: dict[str, list[Any]] = {
     "pck_check_members": [
         _p, _i64, _i64, _p, _p, _p, _p, _f64, _i64, _int, _p, _p, _p, _p,
     ],  # fmt: skip
+    "pck_sampling_check": [
+        _p, _p, _p, _i64, _i64, _i64, _i64, _int, _f64, _f64, _f64, _i64,
+        _p, _p, _p, _p, _p, _p, _p, _p,
+    ],  # fmt: skip
+}
+# size queries, returning int64 (-1 for an invalid argument)
+SIZE_QUERIES: dict[str, list[Any]] = {
+    "pck_sampling_scratch_words": [_i64],
+    "pck_sampling_partial_bytes": [],
 }
 
 
@@ -120,6 +129,10 @@ def lib() -> ctypes.CDLL:
         fn = getattr(handle, name)
         fn.argtypes = argtypes
         fn.restype = _int
+    for name, argtypes in SIZE_QUERIES.items():
+        fn = getattr(handle, name)
+        fn.argtypes = argtypes
+        fn.restype = _i64
     handle.pck_error_string.argtypes = [_int]
     handle.pck_error_string.restype = ctypes.c_char_p
     return handle

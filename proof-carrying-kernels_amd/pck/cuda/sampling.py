@@ -1,0 +1,178 @@
+"""Trusted top-k / top-p set checker on the GPU, and untrusted GPU samplers to test it
+(reference `src/pck/cuda/sampling.py`).
+
+``check_topk_gpu`` and ``check_topp_gpu`` run the library's set checker (`pck_sampling_check`):
+exact FP32 comparisons for the top-k prefix property, FP64 masses for top-p minimality, one
+call for a batch of rows.  Selections are ``(B, L)`` int64 tensors with per-row lengths, so
+top-p nuclei of different sizes share one call.  ``topk_sample``, ``topp_select`` and
+``sharded_topk_gpu`` are the code under test, built from torch operations; they are not
+trusted.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from pck.cuda._lib import check, lib, stream_handle
+from pck.cuda.checker import _check_tensor
+from pck.fp import U32, U64, ceil_div, gamma
+
+BLOCKS_PER_SM = 4  # workgroups per CU the default segment count aims for
+MIN_SEGMENT = 4096  # logits per segment, at least
+
+
+@dataclass(frozen=True)
+class SamplingCheck:
+    """Per-row checker outputs, each of shape (B,) (reference `cuda/sampling.py:26-34`)."""
+
+    passed: torch.Tensor
+    min_selected: torch.Tensor
+    max_rejected: torch.Tensor
+    mass: torch.Tensor
+    mass_without_smallest: torch.Tensor
+
+
+def _lengths(selected: torch.Tensor, lengths: torch.Tensor | None) -> torch.Tensor:
+    if lengths is None:
+        return torch.full((selected.shape[0],), selected.shape[1], dtype=torch.int64, device=selected.device)
+    return lengths
+
+
+def default_segments(logits: torch.Tensor) -> int:
+    """Split each row so that the grid has about ``BLOCKS_PER_SM`` workgroups per CU, with at
+    least ``MIN_SEGMENT`` logits per segment (reference `cuda/sampling.py:43-47`)."""
+    rows, vocab = logits.shape
+    cus = torch.cuda.get_device_properties(logits.device).multi_processor_count
+    return max(1, min(ceil_div(BLOCKS_PER_SM * cus, rows), ceil_div(vocab, MIN_SEGMENT)))
+
+
+def sampling_check(
+    logits: torch.Tensor, selected: torch.Tensor, lengths: torch.Tensor, k: int, top_p: bool,
+    p: float, temperature: float, slack: float, segments: int,
+) -> list[torch.Tensor]:  # fmt: skip
+    """The pybind ``sampling_check`` of the reference (`bindings.cpp:260-298`): the same
+    validation, in the same order and with the same messages; returns
+    [passed, min_selected, max_rejected, mass, mass_without_smallest], enqueued on the
+    current stream."""
+    if not logits.is_cuda:
+        raise RuntimeError("logits must be a CUDA tensor")
+    device = logits.device
+    _check_tensor(logits, "logits", torch.float32, device)
+    _check_tensor(selected, "selected", torch.int64, device)
+    _check_tensor(lengths, "lengths", torch.int64, device)
+    if not (logits.dim() == 2 and selected.dim() == 2 and lengths.dim() == 1):
+        raise RuntimeError("expected logits (B, V), selected (B, L), lengths (B,)")
+    rows, vocab = logits.shape
+    max_len = selected.size(1)
+    if not (selected.size(0) == rows and lengths.size(0) == rows):
+        raise RuntimeError("batch sizes differ")
+    if not (rows >= 1 and vocab >= 1 and max_len >= 1):
+        raise RuntimeError("empty input")
+    if rows > 65535:
+        raise RuntimeError("too many rows")
+    if not (1 <= segments <= vocab and segments <= 2**31 - 1):
+        raise RuntimeError(f"segments must be in [1, V], got {segments}")
+    if not (temperature > 0 and slack >= 0):
+        raise RuntimeError("temperature must be positive, slack >= 0")
+    handle = lib()
+    scratch = torch.zeros((rows, handle.pck_sampling_scratch_words(vocab)), dtype=torch.int32, device=device)
+    partials = torch.empty(rows * segments * handle.pck_sampling_partial_bytes(), dtype=torch.uint8, device=device)
+    passed = torch.empty(rows, dtype=torch.bool, device=device)
+    min_sel = torch.empty(rows, dtype=torch.float32, device=device)
+    max_rej = torch.empty(rows, dtype=torch.float32, device=device)
+    mass = torch.empty(rows, dtype=torch.float64, device=device)
+    without = torch.empty(rows, dtype=torch.float64, device=device)
+    with torch.cuda.device(device):
+        err = handle.pck_sampling_check(
+            logits.data_ptr(), selected.data_ptr(), lengths.data_ptr(), rows, vocab, max_len, k,
+            int(top_p), p, temperature, slack, segments, scratch.data_ptr(), partials.data_ptr(),
+            passed.data_ptr(), min_sel.data_ptr(), max_rej.data_ptr(), mass.data_ptr(),
+            without.data_ptr(), stream_handle(device),
+        )  # fmt: skip
+    check(err, "sampling checker launch")
+    return [passed, min_sel, max_rej, mass, without]
+
+
+def check_topk_gpu(
+    logits: torch.Tensor, selected: torch.Tensor, k: int, segments: int | None = None
+) -> SamplingCheck:
+    """Check that each row of ``selected`` (B, k) is a valid top-k set of ``logits`` (B, V)
+    (reference `cuda/sampling.py:50-58`)."""
+    segs = default_segments(logits) if segments is None else segments
+    out = sampling_check(logits, selected, _lengths(selected, None), k, False, 1.0, 1.0, 0.0, segs)
+    return SamplingCheck(*out)
+
+
+def topp_slack(vocab: int, segments: int, tol: float) -> float:
+    """The sampler's ``tol`` plus this checker's own rounding (reference
+    `cuda/sampling.py:71-88`): each term is FP32 expf on a split argument (within 2 ulp, plus
+    under 2 u32 for the split and the FMA: 6 u32 relative) or below 2^-148 where dropped;
+    each of the S segment partials is rescaled with one FP64 exp, multiply and add; the
+    largest term is exactly 1.  Each mass is then within 16 u32 + V 2^-146 +
+    gamma_{V + 3S + 16}(u64), rounded up."""
+    own = 16 * U32 + math.ldexp(vocab, -146) + gamma(vocab + 3 * segments + 16, U64)
+    return math.nextafter(tol + own, math.inf)
+
+
+def check_topp_gpu(
+    logits: torch.Tensor,
+    selected: torch.Tensor,
+    lengths: torch.Tensor,
+    p: float,
+    temperature: float = 1.0,
+    tol: float = 1e-6,
+    segments: int | None = None,
+) -> SamplingCheck:
+    """Check that ``selected[b, :lengths[b]]`` is a valid, minimal top-p nucleus of row b
+    (reference `cuda/sampling.py:61-93`).  ``tol`` is the sampler's declared probability error;
+    the checker adds its own rounding slack (`topp_slack`)."""
+    if not 0 < p <= 1:
+        raise ValueError(f"p must be in (0, 1], got {p}")
+    if tol < 0:
+        raise ValueError(f"tol must be non-negative, got {tol}")
+    segs = default_segments(logits) if segments is None else segments
+    slack = topp_slack(logits.shape[1], segs, tol)
+    out = sampling_check(logits, selected, lengths, 0, True, p, temperature, slack, segs)
+    return SamplingCheck(*out)
+
+
+def topk_sample(
+    logits: torch.Tensor, k: int, generator: torch.Generator | None = None
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Untrusted sampler: torch.topk, then a draw within the set.  Returns (selected, token)
+    (reference `cuda/sampling.py:96-103`)."""
+    values, idx = torch.topk(logits, k, dim=-1)
+    pick = torch.multinomial(torch.softmax(values, dim=-1), 1, generator=generator)
+    return idx, idx.gather(-1, pick).squeeze(-1)
+
+
+def topp_select(
+    logits: torch.Tensor, p: float, temperature: float = 1.0
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Untrusted top-p (reference `cuda/sampling.py:106-121`): FP32 softmax, a stable
+    descending sort, an FP64 running mass, and the shortest prefix reaching p.  Returns
+    (selected (B, V) sorted indices, lengths (B,)); the first lengths[b] entries of row b are
+    the nucleus."""
+    probs = torch.softmax(logits / temperature, dim=-1)
+    sorted_probs, order = torch.sort(probs, dim=-1, descending=True, stable=True)
+    running = torch.cumsum(sorted_probs.double(), dim=-1)
+    lengths = (running < p).sum(dim=-1) + 1
+    return order.contiguous(), lengths.clamp(max=logits.shape[1]).to(torch.int64)
+
+
+def sharded_topk_gpu(logits: torch.Tensor, k: int, shards: int, per_shard: int) -> torch.Tensor:
+    """Untrusted approximate top-k: the ``per_shard`` largest of each of ``shards`` equal
+    shards, then the k largest of those (the fault model of `pck.faults.sharded_topk`;
+    reference `cuda/sampling.py:124-136`)."""
+    rows, vocab = logits.shape
+    if vocab % shards or per_shard > vocab // shards or k > shards * per_shard:
+        raise ValueError("need vocab % shards == 0, per_shard <= vocab / shards, k <= pool")
+    width = vocab // shards
+    _, local = torch.topk(logits.view(rows, shards, width), per_shard, dim=-1)
+    offsets = torch.arange(shards, device=logits.device).view(1, shards, 1) * width
+    pool = (local + offsets).view(rows, -1)
+    _, pick = torch.topk(logits.gather(-1, pool), k, dim=-1)
+    return pool.gather(-1, pick)

@@ -31,6 +31,8 @@ def test_header_declares_the_entry_points() -> None:
         "pck_gemv_group",
         "pck_blocked_check",
         "pck_check_members",
+        "pck_sampling_check",
+        "pck_sampling_scratch_words",
         "pck_error_string",
     ):
         assert expected in names
@@ -40,7 +42,7 @@ def test_library_exports_every_declared_function() -> None:
     handle = _lib.lib()
     for name in declared_functions():
         assert hasattr(handle, name), name
-    assert set(declared_functions()) >= set(_lib.SIGNATURES)
+    assert set(declared_functions()) >= set(_lib.SIGNATURES) | set(_lib.SIZE_QUERIES)
 
 
 def test_error_strings() -> None:
