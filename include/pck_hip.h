@@ -223,10 +223,15 @@ int pck_check_members(const float* logits, int64_t rows, int64_t vocab, const in
  *   mass_without_smallest (rows,) FP64 (0 unless top-p and the set checks passed).
  * slack is the host's: the sampler's declared error plus this kernel's own rounding.
  * scratch: rows * pck_sampling_scratch_words(vocab) uint32, zero on entry (the caller zeroes it;
- * it holds the selection bitmaps and a malformed flag per row).  partials: rows * segments *
- * pck_sampling_partial_bytes(), 8-byte aligned.  1 <= segments <= vocab, rows <= 65535,
- * temperature > 0, slack >= 0.  Three launches: mark, segment, finish.
+ * it holds the selection bitmaps and a malformed flag per row), needed only when
+ * pck_sampling_needs_scratch(vocab, max_len, segments) returns 1 (selections longer than 4096,
+ * or segments of more than 2^18 logits); otherwise it may be NULL and the segment workgroups
+ * build their bitmaps in LDS.  partials: rows * segments * pck_sampling_partial_bytes(),
+ * 8-byte aligned.  1 <= segments <= vocab, rows <= 65535, temperature > 0, slack >= 0.
+ * Launches: (mark,) segment, finish.  pck_sampling_needs_scratch has no reference counterpart:
+ * the reference always builds the bitmap in zeroed global scratch.
  * -------------------------------------------------------------------------------------------*/
+int pck_sampling_needs_scratch(int64_t vocab, int64_t max_len, int64_t segments);
 int64_t pck_sampling_scratch_words(int64_t vocab);
 int64_t pck_sampling_partial_bytes(void);
 int pck_sampling_check(const float* logits, const int64_t* selected, const int64_t* lengths,

@@ -16,17 +16,22 @@
 // argument alone would lose |d| ulps), 0 for d < -128 (masked -inf logits among them); the
 // sums are FP64.
 //
-// Three launches on the caller's stream; nothing depends on scheduling:
-//   mark:    one lane per selected entry sets its bit in the row's bitmap (caller-zeroed
-//            scratch) with a device-scope atomic OR.  An index out of range, or one whose bit
-//            was already set, marks the row malformed (a plain store of 1 to the row's flag).
-//   segment: a workgroup per (row, segment of ceil(V / S) logits) forms the exact min over the
-//            selected, max over the rejected and over all logits, a NaN flag and, for top-p,
-//            the FP64 sums of e^((l - m_s) / T) over all and over the selected logits relative
-//            to the segment's own maximum m_s, in a fixed order (lane, then wave butterfly,
-//            then waves in order).
-//   finish:  a lane per row merges the segments in order: M = max m_s,
-//            Z = sum z_s e^((m_s - M) / T) (FP64 exp, multiply, add), and decides.
+// Launches on the caller's stream; nothing depends on scheduling:
+//   mark:    (selections longer than kLdsSelect only) one lane per selected entry sets its bit
+//            in the row's bitmap (caller-zeroed scratch) with a device-scope atomic OR.  An
+//            index out of range, or one whose bit was already set, marks the row malformed (a
+//            plain store of 1 to the row's flag).
+//   segment: a workgroup per (row, segment of ceil(V / S) logits).  For selections of at most
+//            kLdsSelect entries it first builds its segment's bitmap in LDS from the selection
+//            itself (LDS atomic OR: a bit already set is a duplicate; segment 0 also flags
+//            indices out of range), so those calls need no scratch and no mark launch.  It then
+//            forms the exact min over the selected, max over the rejected and over all logits,
+//            a NaN flag and, for top-p, the FP64 sums of e^((l - m_s) / T) over all and over
+//            the selected logits relative to the segment's own maximum m_s, in a fixed order
+//            (lane, then wave butterfly, then waves in order).
+//   finish:  a wave per row; lane i merges segments i, i + 64, ... in order (M = max m_s,
+//            z_s e^((m_s - M) / T) with FP64 exp, multiply and add), the lanes meet in a fixed
+//            butterfly, and lane 0 decides.
 // The reference merges in the last segment to finish through an atomic ticket; here a third
 // launch does it, so no workgroup waits on another's writes across the per-XCD L2 caches.
 
@@ -44,10 +49,13 @@ constexpr int kThreads = 256;
 constexpr int kWave = 64;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kAhead = 8;  // logits in flight per lane
+constexpr int64_t kLdsSelect = 4096;      // selections up to this length are read per segment
+constexpr int64_t kLdsBits = 1 << 18;     // the largest segment bitmap kept in LDS (32 KiB)
+constexpr uint32_t kNanFlag = 1u, kMalformedFlag = 2u;
 
 struct Partial {
   float min_sel, max_rej, max_all;
-  uint32_t nan;
+  uint32_t flags;  // kNanFlag, kMalformedFlag
   double z, z_sel;
 };
 static_assert(sizeof(Partial) == 32, "partial layout");
@@ -60,7 +68,7 @@ struct Args {
   int top_p;
   double p, temperature, slack;
   int64_t segments, seg_len, words;
-  uint32_t* bitmap;  // (rows, words)
+  uint32_t* bitmap;  // (rows, words); unused when the selection bitmap is built in LDS
   uint32_t* flags;   // (rows,): nonzero = malformed
   Partial* partials; // (rows, segments)
   uint8_t* passed;
@@ -86,6 +94,32 @@ __global__ void __launch_bounds__(kThreads) mark_kernel(const Args a) {
 
 __device__ __forceinline__ bool selected(const uint32_t* bits, int64_t j) {
   return (bits[j >> 5] >> (j & 31)) & 1u;
+}
+
+// Builds the segment's selection bitmap in LDS from the row's selection (bit j - j0 for index
+// j in [j0, j1)); returns this lane's malformed finding (a duplicate in the segment, or, in
+// segment 0, an index out of range).
+__device__ bool build_lds_bitmap(const Args& a, int64_t row, int64_t seg, int64_t j0,
+                                 int64_t j1, uint32_t* lds) {
+  const int t = static_cast<int>(threadIdx.x);
+  const int64_t words = (j1 - j0 + 31) / 32;
+  for (int64_t w = t; w < words; w += kThreads) lds[w] = 0u;
+  __syncthreads();
+  const int64_t n = a.len[row] < a.max_len ? a.len[row] : a.max_len;
+  const int64_t* sel = a.sel + row * a.max_len;
+  bool bad = false;
+  for (int64_t i = t; i < n; i += kThreads) {
+    const int64_t idx = sel[i];
+    if (idx < 0 || idx >= a.vocab) {
+      bad |= seg == 0;
+    } else if (idx >= j0 && idx < j1) {
+      const int64_t off = idx - j0;
+      const uint32_t bit = 1u << (off & 31);
+      bad |= (atomicOr(&lds[off >> 5], bit) & bit) != 0u;
+    }
+  }
+  __syncthreads();
+  return bad;
 }
 
 // e^d for d = (l - m) / T formed in FP64: FP32 expf of the rounded argument, corrected by the
@@ -116,18 +150,24 @@ __device__ __forceinline__ double wave_sum(double v) {
   return v;
 }
 
+template <bool kLds>
 __global__ void __launch_bounds__(kThreads) segment_kernel(const Args a) {
+  extern __shared__ uint32_t lds_bits[];  // kLds: the segment's bitmap
   __shared__ float fred[3][kWaves];
   __shared__ double dred[2][kWaves];
-  __shared__ uint32_t any_nan;
+  __shared__ uint32_t any_flag;
   const int t = static_cast<int>(threadIdx.x);
   const int wave = t / kWave, lane = t % kWave;
   const int64_t row = blockIdx.y, seg = blockIdx.x;
   const float* l = a.logits + row * a.vocab;
-  const uint32_t* bits = a.bitmap + row * a.words;
-  const int64_t j0 = seg * a.seg_len;
+  const int64_t j0 = seg * a.seg_len < a.vocab ? seg * a.seg_len : a.vocab;
   const int64_t j1 = j0 + a.seg_len < a.vocab ? j0 + a.seg_len : a.vocab;
-  if (t == 0) any_nan = 0u;
+  if (t == 0) any_flag = 0u;
+  bool malformed = false;
+  if constexpr (kLds) malformed = build_lds_bitmap(a, row, seg, j0, j1, lds_bits);
+  // bit of logit j: kLds, bit j - j0 of the LDS bitmap; else bit j of the row's bitmap
+  const uint32_t* bits = kLds ? lds_bits : a.bitmap + row * a.words;
+  const int64_t base = kLds ? j0 : 0;
 
   float mn = INFINITY, mx_rej = -INFINITY, mx = -INFINITY;
   bool nan = false;
@@ -144,7 +184,7 @@ __global__ void __launch_bounds__(kThreads) segment_kernel(const Args a) {
       if (j >= j1) break;
       nan |= x[e] != x[e];
       mx = fmaxf(mx, x[e]);
-      if (selected(bits, j)) mn = fminf(mn, x[e]);
+      if (selected(bits, j - base)) mn = fminf(mn, x[e]);
       else mx_rej = fmaxf(mx_rej, x[e]);
     }
   }
@@ -152,12 +192,14 @@ __global__ void __launch_bounds__(kThreads) segment_kernel(const Args a) {
   mx_rej = wave_max(mx_rej);
   mx = wave_max(mx);
   const bool wave_nan = __any(nan);
-  __syncthreads();  // any_nan is cleared before any wave sets it
+  const bool wave_bad = __any(malformed);
+  __syncthreads();  // any_flag is cleared before any wave sets it
   if (lane == 0) {
     fred[0][wave] = mn;
     fred[1][wave] = mx_rej;
     fred[2][wave] = mx;
-    if (wave_nan) any_nan = 1u;
+    if (wave_nan) atomicOr(&any_flag, kNanFlag);
+    if (wave_bad) atomicOr(&any_flag, kMalformedFlag);
   }
   __syncthreads();
   mn = fred[0][0], mx_rej = fred[1][0], mx = fred[2][0];
@@ -184,7 +226,7 @@ __global__ void __launch_bounds__(kThreads) segment_kernel(const Args a) {
         if (j >= j1) break;
         const double v = term(x[e], m, a.temperature);
         z = z + v;
-        if (selected(bits, j)) z_sel = z_sel + v;
+        if (selected(bits, j - base)) z_sel = z_sel + v;
       }
     }
     z = wave_sum(z);
@@ -197,41 +239,51 @@ __global__ void __launch_bounds__(kThreads) segment_kernel(const Args a) {
     z = (dred[0][0] + dred[0][1]) + (dred[0][2] + dred[0][3]);
     z_sel = (dred[1][0] + dred[1][1]) + (dred[1][2] + dred[1][3]);
   }
-  if (t == 0) a.partials[row * a.segments + seg] = Partial{mn, mx_rej, mx, any_nan, z, z_sel};
+  if (t == 0) a.partials[row * a.segments + seg] = Partial{mn, mx_rej, mx, any_flag, z, z_sel};
 }
 
-__global__ void __launch_bounds__(kThreads) finish_kernel(const Args a) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  if (row >= a.rows) return;
+__global__ void __launch_bounds__(kThreads) finish_kernel(const Args a, int lds_select) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + threadIdx.x / kWave;
+  const int lane = static_cast<int>(threadIdx.x) % kWave;
+  if (row >= a.rows) return;  // whole waves
   const Partial* ps = a.partials + row * a.segments;
   float min_sel = INFINITY, max_rej = -INFINITY, mx = -INFINITY;
-  uint32_t nan = 0u;
-  for (int64_t s = 0; s < a.segments; ++s) {
+  uint32_t flags = 0u;
+  for (int64_t s = lane; s < a.segments; s += kWave) {
     min_sel = fminf(min_sel, ps[s].min_sel);
     max_rej = fmaxf(max_rej, ps[s].max_rej);
     mx = fmaxf(mx, ps[s].max_all);
-    nan |= ps[s].nan;
+    flags |= ps[s].flags;
   }
+  min_sel = wave_min(min_sel);
+  max_rej = wave_max(max_rej);
+  mx = wave_max(mx);
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) flags |= __shfl_xor(flags, o, kWave);
   const int64_t n_sel = a.len[row];
-  const bool well_formed = a.flags[row] == 0u && n_sel >= 1 && n_sel <= a.max_len &&
-                           n_sel <= a.vocab && (a.top_p || n_sel == a.k);
-  bool ok = well_formed && nan == 0u && min_sel >= max_rej;
+  const bool malformed = lds_select ? (flags & kMalformedFlag) != 0u : a.flags[row] != 0u;
+  const bool well_formed = !malformed && n_sel >= 1 && n_sel <= a.max_len && n_sel <= a.vocab &&
+                           (a.top_p || n_sel == a.k);
+  bool ok = well_formed && (flags & kNanFlag) == 0u && min_sel >= max_rej;
   double mass = 0.0, without = 0.0;
-  if (a.top_p && ok) {
+  if (a.top_p && ok) {  // uniform over the wave
     const double big_m = static_cast<double>(mx);
     double big_z = 0.0, big_z_sel = 0.0;
-    for (int64_t s = 0; s < a.segments; ++s) {  // segments in order
+    for (int64_t s = lane; s < a.segments; s += kWave) {  // this lane's segments in order
       if (ps[s].max_all > -INFINITY) {
         const double scale = exp((static_cast<double>(ps[s].max_all) - big_m) / a.temperature);
         big_z = big_z + ps[s].z * scale;
         big_z_sel = big_z_sel + ps[s].z_sel * scale;
       }
     }
+    big_z = wave_sum(big_z);
+    big_z_sel = wave_sum(big_z_sel);
     const double e_min = exp((static_cast<double>(min_sel) - big_m) / a.temperature);
     mass = big_z_sel / big_z;
     without = (big_z_sel - e_min) / big_z;
     ok = mass >= a.p - a.slack && without < a.p + a.slack;
   }
+  if (lane != 0) return;
   a.passed[row] = ok ? 1u : 0u;
   a.min_sel[row] = min_sel;
   a.max_rej[row] = max_rej;
@@ -241,6 +293,12 @@ __global__ void __launch_bounds__(kThreads) finish_kernel(const Args a) {
 
 }  // namespace
 }  // namespace pck
+
+extern "C" int pck_sampling_needs_scratch(int64_t vocab, int64_t max_len, int64_t segments) {
+  if (vocab < 1 || max_len < 1 || segments < 1 || segments > vocab) return -1;
+  const int64_t seg_len = (vocab + segments - 1) / segments;
+  return max_len <= pck::kLdsSelect && seg_len <= pck::kLdsBits ? 0 : 1;
+}
 
 extern "C" int64_t pck_sampling_scratch_words(int64_t vocab) {
   return vocab < 1 ? -1 : (vocab + 31) / 32 + 1;
@@ -258,7 +316,10 @@ extern "C" int pck_sampling_check(const float* logits, const int64_t* selected,
                                   float* min_selected, float* max_rejected, double* mass,
                                   double* mass_without_smallest, void* stream) {
   using namespace pck;
-  if (!logits || !selected || !lengths || !scratch || !partials || !passed || !min_selected ||
+  const int64_t seg_len = (vocab + segments - 1) / segments;
+  const bool lds_select = max_len <= kLdsSelect && seg_len <= kLdsBits;
+  if (!logits || !selected || !lengths || (!scratch && !lds_select) || !partials || !passed ||
+      !min_selected ||
       !max_rejected || !mass || !mass_without_smallest || rows < 1 || rows > 65535 ||
       vocab < 1 || max_len < 1 || segments < 1 || segments > vocab ||
       segments > 0x7FFFFFFF || !(temperature > 0.0) || !(slack >= 0.0) ||
@@ -278,10 +339,10 @@ extern "C" int pck_sampling_check(const float* logits, const int64_t* selected,
   a.temperature = temperature;
   a.slack = slack;
   a.segments = segments;
-  a.seg_len = (vocab + segments - 1) / segments;
+  a.seg_len = seg_len;
   a.words = (vocab + 31) / 32;
   a.bitmap = scratch;
-  a.flags = scratch + rows * a.words;
+  a.flags = scratch ? scratch + rows * a.words : nullptr;
   a.partials = static_cast<Partial*>(partials);
   a.passed = passed;
   a.min_sel = min_selected;
@@ -289,16 +350,22 @@ extern "C" int pck_sampling_check(const float* logits, const int64_t* selected,
   a.mass = mass;
   a.without = mass_without_smallest;
   auto s = static_cast<hipStream_t>(stream);
-  const dim3 mark_grid(static_cast<unsigned>((max_len + kThreads - 1) / kThreads),
-                       static_cast<unsigned>(rows));
-  mark_kernel<<<mark_grid, dim3(kThreads), 0, s>>>(a);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return err;
   const dim3 seg_grid(static_cast<unsigned>(segments), static_cast<unsigned>(rows));
-  segment_kernel<<<seg_grid, dim3(kThreads), 0, s>>>(a);
+  hipError_t err;
+  if (lds_select) {
+    const size_t lds = static_cast<size_t>((seg_len + 31) / 32) * sizeof(uint32_t);
+    segment_kernel<true><<<seg_grid, dim3(kThreads), lds, s>>>(a);
+  } else {
+    const dim3 mark_grid(static_cast<unsigned>((max_len + kThreads - 1) / kThreads),
+                         static_cast<unsigned>(rows));
+    mark_kernel<<<mark_grid, dim3(kThreads), 0, s>>>(a);
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    segment_kernel<false><<<seg_grid, dim3(kThreads), 0, s>>>(a);
+  }
   err = hipGetLastError();
   if (err != hipSuccess) return err;
-  finish_kernel<<<dim3(static_cast<unsigned>((rows + kThreads - 1) / kThreads)), dim3(kThreads),
-                  0, s>>>(a);
+  finish_kernel<<<dim3(static_cast<unsigned>((rows + kWaves - 1) / kWaves)), dim3(kThreads), 0,
+                  s>>>(a, lds_select ? 1 : 0);
   return hipGetLastError();
 }

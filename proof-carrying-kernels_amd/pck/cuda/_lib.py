@@ -133,6 +133,8 @@ def lib() -> ctypes.CDLL:
         fn = getattr(handle, name)
         fn.argtypes = argtypes
         fn.restype = _i64
+    handle.pck_sampling_needs_scratch.argtypes = [_i64, _i64, _i64]
+    handle.pck_sampling_needs_scratch.restype = _int
     handle.pck_error_string.argtypes = [_int]
     handle.pck_error_string.restype = ctypes.c_char_p
     return handle

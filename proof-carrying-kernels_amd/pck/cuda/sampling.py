@@ -78,7 +78,12 @@ def sampling_check(
     if not (temperature > 0 and slack >= 0):
         raise RuntimeError("temperature must be positive, slack >= 0")
     handle = lib()
-    scratch = torch.zeros((rows, handle.pck_sampling_scratch_words(vocab)), dtype=torch.int32, device=device)
+    # short selections are read per segment into LDS; longer ones need the zeroed bitmap
+    if handle.pck_sampling_needs_scratch(vocab, max_len, segments):
+        scratch = torch.zeros((rows, handle.pck_sampling_scratch_words(vocab)), dtype=torch.int32, device=device)
+        scratch_ptr = scratch.data_ptr()
+    else:
+        scratch_ptr = 0
     partials = torch.empty(rows * segments * handle.pck_sampling_partial_bytes(), dtype=torch.uint8, device=device)
     passed = torch.empty(rows, dtype=torch.bool, device=device)
     min_sel = torch.empty(rows, dtype=torch.float32, device=device)
@@ -88,7 +93,7 @@ def sampling_check(
     with torch.cuda.device(device):
         err = handle.pck_sampling_check(
             logits.data_ptr(), selected.data_ptr(), lengths.data_ptr(), rows, vocab, max_len, k,
-            int(top_p), p, temperature, slack, segments, scratch.data_ptr(), partials.data_ptr(),
+            int(top_p), p, temperature, slack, segments, scratch_ptr, partials.data_ptr(),
             passed.data_ptr(), min_sel.data_ptr(), max_rej.data_ptr(), mass.data_ptr(),
             without.data_ptr(), stream_handle(device),
         )  # fmt: skip
