@@ -628,16 +628,24 @@ def main() -> None:
 
     import torch
 
-    from pck.cuda.timing import read_bandwidth_gbps
+    from pck.cuda.timing import read_bandwidth_gbps, read_stream_ms
 
-    gen = torch.Generator().manual_seed(0)
-    print(f"[bench] building {args.copies} BF16 layer copies", file=sys.stderr, flush=True)
-    bf16_layers = build_layers(args.copies, fp8=False, gen=gen)
     bytes_bf16 = sum(gemv_bytes(m, n, 2) for _, m, n in LAYER)
     launch_bytes = {
         launch: sum(gemv_bytes(m, n, 2) for name, m, n in LAYER if name in names)
         for launch, names in LAUNCHES
     }
+    # Read-only streams first, in a fresh address space like the layers' own: the long-stream
+    # ceiling, and each launch's bytes read by one launch (what a launch of that size can reach).
+    print("[bench] timing read-only streams", file=sys.stderr, flush=True)
+    read_ceiling = read_bandwidth_gbps()
+    matched = dict(zip(launch_bytes, read_stream_ms(list(launch_bytes.values())), strict=True))
+    matched_ms = sum(matched.values())
+    torch.cuda.empty_cache()
+
+    gen = torch.Generator().manual_seed(0)
+    print(f"[bench] building {args.copies} BF16 layer copies", file=sys.stderr, flush=True)
+    bf16_layers = build_layers(args.copies, fp8=False, gen=gen)
     # correctness first: every check passes on the honest outputs
     _, results = run_step(bf16_layers[0], True)
     args.steps = max(args.steps, 32)
@@ -680,7 +688,6 @@ def main() -> None:
     ms_checked, ms_gemv_only = ms[MODE_RIDE], ms[MODE_GEMV]
     fp8_checked, fp8_gemv_only = ms8[MODE_RIDE], ms8[MODE_GEMV]
 
-    read_ceiling = read_bandwidth_gbps()
     print("[bench] timing the membership check", file=sys.stderr, flush=True)
     member = membership()
     print("[bench] timing the set-sampling checker", file=sys.stderr, flush=True)
@@ -728,6 +735,10 @@ def main() -> None:
         },
         "eager_launch_ms": {k: round(statistics.mean(v), 5) for k, v in per_launch.items()},
         "hbm_read_ceiling_gbps": round(read_ceiling, 1),
+        "pct_of_read_ceiling": round(100 * value / read_ceiling, 2),
+        "size_matched_read_us": {k: round(1e3 * v, 2) for k, v in matched.items()},
+        "pct_of_size_matched_read": round(100 * matched_ms / ms_checked, 2),
+        "gemv_only_pct_of_size_matched_read": round(100 * matched_ms / ms_gemv_only, 2),
         "membership": member,
         "sampling": sampling,
         "batched": batched,

@@ -241,9 +241,11 @@ int pck_sampling_check(const float* logits, const int64_t* selected, const int64
                        float* max_rejected, double* mass, double* mass_without_smallest,
                        void* stream);
 
-/* Measurement: reads `bytes` (a multiple of 16, 16-byte aligned) from `src` with `groups`
- * workgroups of 256 lanes and stores one word per workgroup into sink[groups].  The practical
- * HBM read ceiling for the GEMV roofline; no reference counterpart (the reference measures a
+/* Measurement: reads `bytes` (a multiple of 16, 16-byte aligned) from `src`, workgroup g of
+ * `groups` (256 lanes, 4 waves each) one contiguous chunk of ceil(bytes / 16 / groups) 16-byte
+ * vectors rounded up to a multiple of 2048, and stores one word per wave into sink[4 * groups]
+ * (their XOR is the XOR of every 32-bit word read).  The practical HBM read ceiling for the GEMV
+ * roofline (use 64 KiB per workgroup); no reference counterpart (the reference measures a
  * device-to-device copy, src/pck/cuda/timing.py:50-55). */
 int pck_read_stream(const void* src, int64_t bytes, uint32_t* sink, int groups, void* stream);
 

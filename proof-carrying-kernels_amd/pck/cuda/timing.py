@@ -68,31 +68,51 @@ def copy_bandwidth_gbps(timer: ColdL2Timer, nbytes: int = 1 << 30) -> float:
     return float(2 * src.numel() / (t.median_ms / 1e3) / 1e9)
 
 
+READ_CHUNK = 64 << 10  # bytes per workgroup of the read stream (fastest measured on MI355X)
+
+
+def read_stream_ms(sizes: list[int], total: int = 1 << 30, reps: int = 20) -> list[float]:
+    """Mean time of one `pck_read_stream` launch over ``sizes[i]`` bytes: enough buffers of
+    each size to span ``total`` bytes (more than L2 + MALL) are read one after another from a
+    captured HIP graph, so every launch streams from HBM and the host launch rate plays no part
+    (the GEMV passes it is compared with are graph replays too).  The read-only ceiling of a
+    launch of that many bytes."""
+    from pck.cuda._lib import check, lib
+
+    handle = lib()
+    out = []
+    for size in sizes:
+        size = size // 16 * 16
+        bufs = [torch.ones(size, dtype=torch.uint8, device="cuda") for _ in range(max(1, -(-total // size)))]
+        groups = max(1, -(-size // READ_CHUNK))
+        sink = torch.empty(4 * groups, dtype=torch.int32, device="cuda")
+
+        def read_all() -> None:
+            stream = torch.cuda.current_stream().cuda_stream
+            for src in bufs:
+                err = handle.pck_read_stream(src.data_ptr(), size, sink.data_ptr(), groups, stream)
+                check(err, "read stream")
+
+        read_all()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            read_all()
+        graph.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        out.append(start.elapsed_time(end) / (reps * len(bufs)))
+        del graph, bufs
+    return out
+
+
 def read_bandwidth_gbps(nbytes: int = 2 << 30, reps: int = 20) -> float:
-    """Read-only streaming bandwidth of the `pck_read_stream` kernel over a buffer larger
-    than L2 + MALL: the practical HBM read ceiling of the GEMVs."""
-    from pck.cuda._lib import check, lib, stream_handle
-
-    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
-    src.fill_(1)
-    cus = torch.cuda.get_device_properties(0).multi_processor_count
-    groups = 8 * cus
-    sink = torch.empty(groups, dtype=torch.int32, device="cuda")
-
-    def run() -> None:
-        check(
-            lib().pck_read_stream(
-                src.data_ptr(), nbytes, sink.data_ptr(), groups, stream_handle(src.device)
-            ),
-            "read stream",
-        )
-
-    for _ in range(3):
-        run()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(reps):
-        run()
-    end.record()
-    torch.cuda.synchronize()
-    return nbytes * reps / (start.elapsed_time(end) / 1e3) / 1e9
+    """Read-only streaming bandwidth of `pck_read_stream` over one 2 GiB buffer (larger than
+    L2 + MALL): the long-stream HBM read ceiling."""
+    (ms,) = read_stream_ms([nbytes], total=nbytes, reps=reps)
+    return nbytes / (ms / 1e3) / 1e9
