@@ -641,6 +641,12 @@ def main() -> None:
     read_ceiling = read_bandwidth_gbps()
     matched = dict(zip(launch_bytes, read_stream_ms(list(launch_bytes.values())), strict=True))
     matched_ms = sum(matched.values())
+    launch_bytes8 = {
+        launch: sum(gemv_bytes(m, n, 1) for name, m, n in LAYER if name in names)
+        for launch, names in LAUNCHES
+    }
+    matched8 = dict(zip(launch_bytes8, read_stream_ms(list(launch_bytes8.values())), strict=True))
+    matched8_ms = sum(matched8.values())
     torch.cuda.empty_cache()
 
     gen = torch.Generator().manual_seed(0)
@@ -732,6 +738,9 @@ def main() -> None:
                 100 * (ms8[MODE_OVERLAP] / fp8_gemv_only - 1), 2
             ),
             "ms_per_step": round(fp8_checked, 5),
+            "size_matched_read_us": {k: round(1e3 * v, 2) for k, v in matched8.items()},
+            "pct_of_size_matched_read": round(100 * matched8_ms / fp8_checked, 2),
+            "gemv_only_pct_of_size_matched_read": round(100 * matched8_ms / fp8_gemv_only, 2),
         },
         "eager_launch_ms": {k: round(statistics.mean(v), 5) for k, v in per_launch.items()},
         "hbm_read_ceiling_gbps": round(read_ceiling, 1),
