@@ -312,33 +312,50 @@ __global__ void __launch_bounds__(kThreads) finish_kernel(const Plan plan) {
   const int groups = static_cast<int>(d.block / 4);  // block % 4 == 0
   const int segments = static_cast<int>(plan.segments[g]);
   const int64_t outs = d.checks * d.num_blocks * d.batch;
+  // Every load below is unconditional, at a valid address (a column past the batch reads
+  // column 0, a group or segment past the end reads the last one), and data that is not needed
+  // is dropped where it is used: a conditional load would be followed by a wait for it before
+  // the next one could be issued.  The sums of columns past the batch are computed and never
+  // read.
   const float4* ycol[kRowCols];
-  bool live[kRowCols];  // the same for the whole row of 16 lanes
 #pragma unroll
   for (int j = 0; j < kRowCols; ++j) {
     const int64_t col = col0 + row + kFinishLanes * j;
-    live[j] = col < d.batch;
-    ycol[j] = reinterpret_cast<const float4*>(d.Y + (live[j] ? col : 0) * m + beta * d.block);
+    ycol[j] = reinterpret_cast<const float4*>(d.Y + (col < d.batch ? col : 0) * m + beta * d.block);
   }
 
   // sum |y| to nearest, at most block / 16 + 4 additions deep, then raised by 1 + (b + 4) 2^-52
   // (the factor is exact in FP64)
   const double yabs_slack = 1.0 + static_cast<double>(d.block + 4) * 0x1p-52;
   double yabs[kRowCols] = {};
+  const int pc = t % kFinishCols, sub = t / kFinishCols;  // partials: column, segment subset
+  const bool pin = col0 + pc < d.batch;
+  constexpr int kAhead = 8;
   for (int64_t k = 0; k < d.checks; ++k) {
     const int64_t pair = k * d.num_blocks + beta;
     const uint32_t* sign = reinterpret_cast<const uint32_t*>(d.r + pair * d.block);
+    // The first pass of this lane's partials (column t % 64, segments t / 64, t / 64 + 4, ...)
+    // is requested before the outputs, so both reads are in flight together.
+    const int64_t pat = pair * d.batch + (pin ? col0 + pc : 0);
+    const double* pcx = plan.part_cx + plan.slots[g] + pat;
+    const double* ps = plan.part_s + plan.slots[g] + pat;
+    double vc[kAhead], vs[kAhead];
+#pragma unroll
+    for (int e = 0; e < kAhead; ++e) {
+      const int sgi = sub + kSubsets * e < segments ? sub + kSubsets * e : segments - 1;
+      vc[e] = pcx[sgi * outs];
+      vs[e] = ps[sgi * outs];
+    }
     double ry[kRowCols] = {};
     for (int i0 = q; i0 < groups; i0 += kPass * kFinishLanes) {
       float4 v[kRowCols][kPass];
       uint32_t sg[kPass];
 #pragma unroll
       for (int e = 0; e < kPass; ++e) {
-        const int i = i0 + kFinishLanes * e;
-        sg[e] = i < groups ? sign[i] : 0x01010101u;
+        const int i = i0 + kFinishLanes * e < groups ? i0 + kFinishLanes * e : groups - 1;
+        sg[e] = sign[i];
 #pragma unroll
-        for (int j = 0; j < kRowCols; ++j)
-          v[j][e] = (live[j] && i < groups) ? ycol[j][i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int j = 0; j < kRowCols; ++j) v[j][e] = ycol[j][i];
       }
 #pragma unroll
       for (int e = 0; e < kPass; ++e) {
@@ -366,32 +383,27 @@ __global__ void __launch_bounds__(kThreads) finish_kernel(const Plan plan) {
       }
     }
 
-    // Partials: column t % 64, segments t / 64, t / 64 + 4, ...
+    // Partials, in the order of the segments: the first pass loaded above, later passes here.
     {
-      const int c = t % kFinishCols, sub = t / kFinishCols;
-      const bool in = col0 + c < d.batch;
-      const int64_t at = pair * d.batch + col0 + c;
-      const double* pcx = plan.part_cx + plan.slots[g] + at;
-      const double* ps = plan.part_s + plan.slots[g] + at;
       double cx = 0.0, s = 0.0;
-      constexpr int kAhead = 8;
-      for (int s0 = sub; s0 < segments; s0 += kAhead * kSubsets) {
-        double vc[kAhead], vs[kAhead];
-#pragma unroll
-        for (int e = 0; e < kAhead; ++e) {
-          const int sgi = s0 + kSubsets * e;
-          vc[e] = (in && sgi < segments) ? pcx[sgi * outs] : 0.0;
-          vs[e] = (in && sgi < segments) ? ps[sgi * outs] : 0.0;
-        }
+      for (int s0 = sub;;) {
 #pragma unroll
         for (int e = 0; e < kAhead; ++e) {
           if (s0 + kSubsets * e >= segments) break;
           cx = cx + vc[e];
           s = s + vs[e];
         }
+        s0 += kAhead * kSubsets;
+        if (s0 >= segments) break;
+#pragma unroll
+        for (int e = 0; e < kAhead; ++e) {
+          const int sgi = s0 + kSubsets * e < segments ? s0 + kSubsets * e : segments - 1;
+          vc[e] = pcx[sgi * outs];
+          vs[e] = ps[sgi * outs];
+        }
       }
-      red_cx[sub][c] = cx;
-      red_s[sub][c] = s;
+      red_cx[sub][pc] = cx;
+      red_s[sub][pc] = s;
     }
     __syncthreads();
     if (t < kFinishCols && col0 + t < d.batch) {
