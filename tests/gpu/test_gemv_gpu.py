@@ -117,15 +117,14 @@ def test_llama_shapes_bit_exact(m: int, n: int) -> None:
 
 
 SHAPE_KNOBS = [(0, 0, 0)] + [(r, u, nt) for r in (1, 2, 4) for u in (1, 2, 4) for nt in (0, 1)]
+# Thread counts other than 256 have a single launch shape, the built-in one.
+LAUNCHES = [(256, shape) for shape in SHAPE_KNOBS] + [(t, (0, 0, 0)) for t in (32, 64, 128, 512, 1024)]
 
 
-@pytest.mark.parametrize("threads", [32, 64, 128, 256, 512, 1024])
-@pytest.mark.parametrize("shape", SHAPE_KNOBS, ids=str)
+@pytest.mark.parametrize(("threads", "shape"), LAUNCHES, ids=str)
 def test_every_launch_shape_gives_the_same_bits(threads: int, shape: tuple[int, int, int]) -> None:
     """rows per wave, loads ahead and non-temporal loads change only speed ((0, 0, 0) = the
-    built-in choice; thread counts other than 256 have a single shape)."""
-    if threads != 256 and shape != (0, 0, 0):
-        pytest.skip("one launch shape below / above 256 threads")
+    built-in choice)."""
     W, x = random_problem(77, 3000 + threads, seed=threads)
     want = gemv_coalesced_c(W, x, threads)
     try:
