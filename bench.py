@@ -564,46 +564,67 @@ def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: in
     return out
 
 
-def cpu_baseline(budget_s: float = 10.0) -> dict:
-    """The oracle on this host, on one core: the coalesced-tree CPU model of every projection of
-    the decode layer (T = 256) plus the CPU blocked checker at b = 128, K = 1, repeated over
-    whole layers until ``budget_s`` seconds of CPU work have run; GB/s of the same metric (GEMV
-    algorithmic bytes / time).  BLAS is held to one thread so the figure is one core's."""
+def host_cpu() -> str:
+    """The host CPU's model name, as /proc/cpuinfo gives it."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(budget_s: float = 10.0, fp8: bool = False, all_cores: bool = False) -> dict:
+    """The oracle on this host: the coalesced-tree CPU model of every projection of the decode
+    layer (T = 256) plus the CPU blocked checker at b = 128, K = 1, repeated over whole layers
+    until ``budget_s`` seconds have run; GB/s of the same metric (GEMV algorithmic bytes /
+    time).  One core: the NumPy model with BLAS held to one thread.  All cores: the scalar C
+    model (OpenMP over rows) with BLAS on every thread.  FP8: E4M3 weights quantized per row
+    by torch on the CPU (the GPU path's quantizer), the model with 16-byte vectors of 16
+    codes, the checker on the E4M3 values."""
     import numpy as np
-    from threadpoolctl import threadpool_limits
+    import torch
+    from threadpoolctl import threadpool_info, threadpool_limits
 
     from oracle.checker import BlockedChecker
+    from oracle.cmodel import gemv_coalesced_c
     from oracle.gemv import emulate_gemv_coalesced
+    from pck.cuda.gemv import quantize_fp8
     from pck.fp import bf16, tree_height
 
+    vec = 16 if fp8 else 8
     rng = np.random.default_rng(0)
-    layer = [
-        (bf16(rng.standard_normal((m, n), dtype=np.float32) * np.float32(0.02)),
-         bf16(rng.standard_normal(n, dtype=np.float32)))
-        for _, m, n in LAYER
-    ]  # fmt: skip
-    nbytes = sum(gemv_bytes(m, n, 2) for _, m, n in LAYER)
+    layer = []
+    for _, m, n in LAYER:
+        W = bf16(rng.standard_normal((m, n), dtype=np.float32) * np.float32(0.02))
+        if fp8:
+            W = quantize_fp8(torch.from_numpy(W))[0].float().numpy()
+        layer.append((W, bf16(rng.standard_normal(n, dtype=np.float32))))
+    nbytes = sum(gemv_bytes(m, n, 1 if fp8 else 2) for _, m, n in LAYER)
+    blas = max((info.get("num_threads", 1) for info in threadpool_info()), default=1)
     passes, elapsed = 0, 0.0
-    with threadpool_limits(limits=1):
+    with threadpool_limits(limits=None if all_cores else 1):
         while elapsed < budget_s:
             t0 = time.perf_counter()
             for W, x in layer:
                 m, n = W.shape
-                y = emulate_gemv_coalesced(W, x, THREADS)
-                ok = BlockedChecker(W, x, BLOCK, tree_height(n, THREADS, 8)).verdict(
-                    y, rng, checks=1
-                )
+                y = gemv_coalesced_c(W, x, THREADS, vec) if all_cores else emulate_gemv_coalesced(W, x, THREADS, vec)
+                ok = BlockedChecker(W, x, BLOCK, tree_height(n, THREADS, vec)).verdict(y, rng, checks=1)
                 assert ok.all()
             elapsed += time.perf_counter() - t0
             passes += 1
+    cores = os.cpu_count() or 1
+    model = "scalar C model (OpenMP over rows)" if all_cores else "NumPy emulate_gemv_coalesced"
     return {
         "value": round(passes * nbytes / elapsed / 1e9, 3),
         "unit": "GB/s",
-        "cores": 1,
+        "cores": cores if all_cores else 1,
         "kind": "port",
-        "sample": f"oracle emulate_gemv_coalesced + BlockedChecker.verdict (K=1, b=128) over "
-        f"the 7 projections of the layer, {passes} layer passes in {elapsed:.1f} s, one thread "
-        f"(BLAS limited to 1), host has {os.cpu_count()} CPUs",
+        "sample": f"oracle {model} + BlockedChecker.verdict (K=1, b=128) over the 7 "
+        f"{'FP8' if fp8 else 'BF16'} projections of the layer, {passes} layer passes in "
+        f"{elapsed:.1f} s, {'all threads' if all_cores else 'one thread'} (BLAS "
+        f"{blas if all_cores else 1} of {blas} threads); host: {cores} CPUs, {host_cpu()}",
     }
 
 
@@ -764,8 +785,10 @@ def main() -> None:
         },
     }
     if not args.no_cpu_baseline:
-        print("[bench] timing the CPU baseline", file=sys.stderr, flush=True)
+        print("[bench] timing the CPU baselines", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline()
+        line["cpu_baseline_all_cores"] = cpu_baseline(all_cores=True)
+        line["fp8"]["cpu_baseline"] = cpu_baseline(fp8=True)
     print(json.dumps(line), flush=True)
 
 
