@@ -108,14 +108,25 @@ __device__ bool build_lds_bitmap(const Args& a, int64_t row, int64_t seg, int64_
   const int64_t n = a.len[row] < a.max_len ? a.len[row] : a.max_len;
   const int64_t* sel = a.sel + row * a.max_len;
   bool bad = false;
-  for (int64_t i = t; i < n; i += kThreads) {
-    const int64_t idx = sel[i];
-    if (idx < 0 || idx >= a.vocab) {
-      bad |= seg == 0;
-    } else if (idx >= j0 && idx < j1) {
-      const int64_t off = idx - j0;
-      const uint32_t bit = 1u << (off & 31);
-      bad |= (atomicOr(&lds[off >> 5], bit) & bit) != 0u;
+  // kAhead entries per lane in flight; an entry past the end reads the last one (never used)
+  for (int64_t i0 = t; i0 < n; i0 += kAhead * kThreads) {
+    int64_t v[kAhead];
+#pragma unroll
+    for (int e = 0; e < kAhead; ++e) {
+      const int64_t i = i0 + static_cast<int64_t>(e) * kThreads;
+      v[e] = sel[i < n ? i : n - 1];
+    }
+#pragma unroll
+    for (int e = 0; e < kAhead; ++e) {
+      if (i0 + static_cast<int64_t>(e) * kThreads >= n) break;
+      const int64_t idx = v[e];
+      if (idx < 0 || idx >= a.vocab) {
+        bad |= seg == 0;
+      } else if (idx >= j0 && idx < j1) {
+        const int64_t off = idx - j0;
+        const uint32_t bit = 1u << (off & 31);
+        bad |= (atomicOr(&lds[off >> 5], bit) & bit) != 0u;
+      }
     }
   }
   __syncthreads();
@@ -176,7 +187,7 @@ __global__ void __launch_bounds__(kThreads) segment_kernel(const Args a) {
 #pragma unroll
     for (int e = 0; e < kAhead; ++e) {
       const int64_t j = jb + static_cast<int64_t>(e) * kThreads;
-      x[e] = j < j1 ? l[j] : -INFINITY;
+      x[e] = l[j < j1 ? j : j1 - 1];  // past the segment: a valid address, never used
     }
 #pragma unroll
     for (int e = 0; e < kAhead; ++e) {
@@ -218,7 +229,7 @@ __global__ void __launch_bounds__(kThreads) segment_kernel(const Args a) {
 #pragma unroll
       for (int e = 0; e < kAhead; ++e) {
         const int64_t j = jb + static_cast<int64_t>(e) * kThreads;
-        x[e] = j < j1 ? l[j] : -INFINITY;
+        x[e] = l[j < j1 ? j : j1 - 1];  // past the segment: a valid address, never used
       }
 #pragma unroll
       for (int e = 0; e < kAhead; ++e) {

@@ -193,3 +193,28 @@ def test_masked_minus_inf_logits_do_not_raise_false_alarms() -> None:
     for b in range(4):
         sel = selected[b, : lengths[b]].cpu().numpy()
         assert check_topp(lg[b].cpu().numpy(), sel, 0.9, tol=1e-5)
+
+
+def test_short_and_long_nuclei_in_one_call_match_cpu() -> None:
+    """Nuclei of a few thousand and of over a hundred thousand entries in one call, with a
+    duplicate planted in one row of each kind and an out-of-range index in another long row:
+    every row gets the CPU checker's verdict."""
+    rows, vocab = 6, 151_936
+    lg = logits(rows, vocab, seed=31, scale=3.0)  # nuclei of about 6,600 entries
+    lg[3:] *= 0.01  # nearly flat rows: nuclei of most of the vocabulary
+    selected, lengths = topp_select(lg, 0.9)
+    n = lengths.cpu()
+    assert bool((n[:3] < 10_000).all()) and bool((n[3:] > 100_000).all())
+    bad = selected.clone()
+    bad[1, 1] = bad[1, 0]  # duplicate, short row
+    bad[4, 1] = bad[4, 0]  # duplicate, long row
+    bad[5, 2] = vocab  # out of range, long row
+    res = check_topp_gpu(lg, bad, lengths, 0.9, tol=1e-5)
+    cpu = [
+        check_topp(lg[b].cpu().numpy(), bad[b, : lengths[b]].cpu().numpy(), 0.9, tol=1e-5)
+        for b in range(rows)
+    ]
+    np.testing.assert_array_equal(res.passed.cpu().numpy(), cpu)
+    assert cpu == [True, False, True, True, False, False]
+    honest = check_topp_gpu(lg, selected, lengths, 0.9, tol=1e-5)
+    assert honest.passed.all()
