@@ -26,9 +26,12 @@ Printed JSON line:
                  from two rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE), as recorded in
                  the committed summary named by traffic_source
   cpu_baseline   the oracle's CPU model of the same work (coalesced-tree GEMV + CPU blocked
-                 checker) timed on this host on a bounded sample
+                 checker) timed on this host on a bounded sample, one core (the all-core C
+                 model in cpu_baseline_all_cores, the FP8 layer in fp8.cpu_baseline)
 plus the FP8 layer, GEMV-only times, the checker overhead, the membership check (256 x 151936
-logits) and a read-only stream ceiling.
+logits), the set-sampling checker, the batched layer (B = 128, 256) and the read-only stream
+ceilings: the long stream (hbm_read_ceiling_gbps) and one launch over each GEMV launch's bytes
+(size_matched_read_us; pct_of_size_matched_read is their sum over the layer's time).
 
 Run: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--quick]
 """
