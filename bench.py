@@ -419,7 +419,7 @@ BATCHED_LAUNCHES = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense BF16 matrix peak
 
 
-def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: int = 2) -> dict:
+def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: int = 7) -> dict:
     """BASELINE config 4 read literally: a Llama-3-8B decode layer at batch B = 128 and 256 on
     the matrix cores (four packed launches: q/k/v, o, gate/up, down; BF16 and FP8 weights),
     every column of every output checked by one batched checker launch per layer (b = 128,
@@ -457,7 +457,7 @@ def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: in
         res = check_batched([(ch, X, Y) for (_, ch), X, Y in zip(layer, xs, ys)]) if with_check else None
         return ys, res
 
-    def time_pass(fn) -> float:  # type: ignore[no-untyped-def]
+    def capture_pass(fn):  # type: ignore[no-untyped-def]
         warm = torch.cuda.Stream()
         warm.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(warm):
@@ -469,13 +469,21 @@ def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: in
             fn()
         g.replay()
         torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
+        return g
+
+    def time_passes(graphs: list) -> list[float]:  # type: ignore[type-arg]
+        """ms per layer of each captured pass: the passes replayed in turn, ``reps`` rounds,
+        the median per pass (so a drift of the clocks does not favour either)."""
+        times: list[list[float]] = [[] for _ in graphs]
         for _ in range(reps):
-            g.replay()
-        b.record()
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / (reps * depth)
+            for i, g in enumerate(graphs):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                g.replay()
+                b.record()
+                torch.cuda.synchronize()
+                times[i].append(a.elapsed_time(b) / depth)
+        return [statistics.median(t) for t in times]
 
     out = {}
     for B in batches:
@@ -485,8 +493,10 @@ def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: in
             ls = layers[fp8]
             ys, res = run_layer(ls[0], xs, True)
             assert all(bool(r.passed.all()) for r in res), "batched checker rejected an honest output"
-            ms_gemm = time_pass(lambda: [run_layer(ls[i % copies], xs, False) for i in range(depth)])
-            ms_chk = time_pass(lambda: [run_layer(ls[i % copies], xs, True) for i in range(depth)])
+            g_gemm = capture_pass(lambda: [run_layer(ls[i % copies], xs, False) for i in range(depth)])
+            g_chk = capture_pass(lambda: [run_layer(ls[i % copies], xs, True) for i in range(depth)])
+            ms_gemm, ms_chk = time_passes([g_gemm, g_chk])
+            del g_gemm, g_chk
             # fault campaign on copy 0: every (block, column) cell of every output, per kind
             # (reference fault set, harness/numerics_sim.py:58-64 and harness/campaign.py:8-13)
             rng = np.random.default_rng(B + fp8)
@@ -561,7 +571,9 @@ def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: in
                 "false_alarms": false_alarms,
                 "honest_cells": cells,
             }
-        ms_blas = time_pass(lambda: [[torch.mm(X, W.t()) for W, X in zip(raw[i % copies], xs)] for i in range(depth)])
+        g_blas = capture_pass(lambda: [[torch.mm(X, W.t()) for W, X in zip(raw[i % copies], xs)] for i in range(depth)])
+        (ms_blas,) = time_passes([g_blas])
+        del g_blas
         entry["hipblaslt_ms_per_layer"] = round(ms_blas, 5)
         out[f"B{B}"] = entry
     return out
