@@ -452,10 +452,24 @@ def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: in
         layers[False].append(l16)
         layers[True].append(l8)
 
-    def run_layer(layer, xs, with_check: bool):  # type: ignore[no-untyped-def]
+    def run_layer(layer, xs, with_check: bool, side=None):  # type: ignore[no-untyped-def]
+        """One layer; with ``side`` its check runs on that stream after the layer's products
+        (an event orders it), overlapping the next layer's products, as the reference's
+        SideStreamChecker overlaps checks (src/pck/cuda/checker.py:174-215)."""
         ys = [gemm_batched(Wp, X) for (Wp, _), X in zip(layer, xs)]
-        res = check_batched([(ch, X, Y) for (_, ch), X, Y in zip(layer, xs, ys)]) if with_check else None
+        if not with_check:
+            return ys, None
+        if side is None:
+            return ys, check_batched([(ch, X, Y) for (_, ch), X, Y in zip(layer, xs, ys)])
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            res = check_batched([(ch, X, Y) for (_, ch), X, Y in zip(layer, xs, ys)])
         return ys, res
+
+    def side_pass(ls, xs, side):  # type: ignore[no-untyped-def]
+        out = [run_layer(ls[i % copies], xs, True, side) for i in range(depth)]
+        torch.cuda.current_stream().wait_stream(side)  # the pass ends after its last check
+        return out
 
     def capture_pass(fn):  # type: ignore[no-untyped-def]
         warm = torch.cuda.Stream()
@@ -493,10 +507,12 @@ def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: in
             ls = layers[fp8]
             ys, res = run_layer(ls[0], xs, True)
             assert all(bool(r.passed.all()) for r in res), "batched checker rejected an honest output"
+            side = torch.cuda.Stream()
             g_gemm = capture_pass(lambda: [run_layer(ls[i % copies], xs, False) for i in range(depth)])
             g_chk = capture_pass(lambda: [run_layer(ls[i % copies], xs, True) for i in range(depth)])
-            ms_gemm, ms_chk = time_passes([g_gemm, g_chk])
-            del g_gemm, g_chk
+            g_side = capture_pass(lambda: side_pass(ls, xs, side))  # noqa: B023
+            ms_gemm, ms_chk, ms_side = time_passes([g_gemm, g_chk, g_side])
+            del g_gemm, g_chk, g_side
             # fault campaign on copy 0: every (block, column) cell of every output, per kind
             # (reference fault set, harness/numerics_sim.py:58-64 and harness/campaign.py:8-13)
             rng = np.random.default_rng(B + fp8)
@@ -561,6 +577,7 @@ def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: in
                 "gemm_only_tflops": round(B * flops_per_row / (ms_gemm / 1e3) / 1e12, 1),
                 "mfma_peak_frac": round(B * flops_per_row / (ms_gemm / 1e3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
                 "checker_overhead_pct": round(100 * (ms_chk / ms_gemm - 1), 2),
+                "checker_overhead_side_stream_pct": round(100 * (ms_side / ms_gemm - 1), 2),
                 "faulty_columns": planted,  # per kind and launch: every column has the fault
                 "faulty_columns_caught": caught,
                 "faults_by_kind": {
