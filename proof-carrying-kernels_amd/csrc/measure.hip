@@ -43,7 +43,8 @@ __global__ void __launch_bounds__(kThreads)
     acc ^= a[0] ^ a[1] ^ a[2] ^ a[3];
   }
   for (int off = 32; off > 0; off /= 2) acc ^= __shfl_xor(acc, off, 64);
-  if ((threadIdx.x & 63) == 0) sink[blockIdx.x * (kThreads / 64) + threadIdx.x / 64] = acc;
+  if ((threadIdx.x & 63) == 0)
+    sink[static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + threadIdx.x / 64] = acc;
 }
 
 }  // namespace
