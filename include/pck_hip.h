@@ -222,6 +222,8 @@ int pck_check_members(const float* logits, int64_t rows, int64_t vocab, const in
  *   passed (rows,) uint8; min_selected, max_rejected (rows,) FP32, exact; mass and
  *   mass_without_smallest (rows,) FP64 (0 unless top-p and the set checks passed).
  * slack is the host's: the sampler's declared error plus this kernel's own rounding.
+ * lengths (rows,) int64, or NULL: every row's selection is all max_len entries (a top-k call;
+ * the reference passes a tensor filled with k).
  * scratch: rows * pck_sampling_scratch_words(vocab) uint32, zero on entry (the caller zeroes it;
  * it holds the selection bitmaps and a malformed flag per row), needed only when
  * pck_sampling_needs_scratch(vocab, max_len, segments) returns 1 (selections longer than 4096,

@@ -63,7 +63,7 @@ static_assert(sizeof(Partial) == 32, "partial layout");
 struct Args {
   const float* logits;
   const int64_t* sel;
-  const int64_t* len;
+  const int64_t* len;  // (rows,), or NULL: every row is max_len long
   int64_t rows, vocab, max_len, k;
   int top_p;
   double p, temperature, slack;
@@ -78,10 +78,15 @@ struct Args {
   double* without;
 };
 
+// The selection length of a row (every row is max_len long without a lengths array).
+__device__ __forceinline__ int64_t row_length(const Args& a, int64_t row) {
+  return a.len ? a.len[row] : a.max_len;
+}
+
 __global__ void __launch_bounds__(kThreads) mark_kernel(const Args a) {
   const int64_t row = blockIdx.y;
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  const int64_t n = a.len[row] < a.max_len ? a.len[row] : a.max_len;
+  const int64_t n = row_length(a, row) < a.max_len ? row_length(a, row) : a.max_len;
   if (i >= n) return;
   const int64_t idx = a.sel[row * a.max_len + i];
   if (idx < 0 || idx >= a.vocab) {
@@ -105,7 +110,7 @@ __device__ bool build_lds_bitmap(const Args& a, int64_t row, int64_t seg, int64_
   const int64_t words = (j1 - j0 + 31) / 32;
   for (int64_t w = t; w < words; w += kThreads) lds[w] = 0u;
   __syncthreads();
-  const int64_t n = a.len[row] < a.max_len ? a.len[row] : a.max_len;
+  const int64_t n = row_length(a, row) < a.max_len ? row_length(a, row) : a.max_len;
   const int64_t* sel = a.sel + row * a.max_len;
   bool bad = false;
   // kAhead entries per lane in flight; an entry past the end reads the last one (never used)
@@ -271,7 +276,7 @@ __global__ void __launch_bounds__(kThreads) finish_kernel(const Args a, int lds_
   mx = wave_max(mx);
 #pragma unroll
   for (int o = 1; o < kWave; o <<= 1) flags |= __shfl_xor(flags, o, kWave);
-  const int64_t n_sel = a.len[row];
+  const int64_t n_sel = row_length(a, row);
   const bool malformed = lds_select ? (flags & kMalformedFlag) != 0u : a.flags[row] != 0u;
   const bool well_formed = !malformed && n_sel >= 1 && n_sel <= a.max_len && n_sel <= a.vocab &&
                            (a.top_p || n_sel == a.k);
@@ -329,7 +334,7 @@ extern "C" int pck_sampling_check(const float* logits, const int64_t* selected,
   using namespace pck;
   const int64_t seg_len = (vocab + segments - 1) / segments;
   const bool lds_select = max_len <= kLdsSelect && seg_len <= kLdsBits;
-  if (!logits || !selected || !lengths || (!scratch && !lds_select) || !partials || !passed ||
+  if (!logits || !selected || (!scratch && !lds_select) || !partials || !passed ||
       !min_selected ||
       !max_rejected || !mass || !mass_without_smallest || rows < 1 || rows > 65535 ||
       vocab < 1 || max_len < 1 || segments < 1 || segments > vocab ||

@@ -35,12 +35,6 @@ class SamplingCheck:
     mass_without_smallest: torch.Tensor
 
 
-def _lengths(selected: torch.Tensor, lengths: torch.Tensor | None) -> torch.Tensor:
-    if lengths is None:
-        return torch.full((selected.shape[0],), selected.shape[1], dtype=torch.int64, device=selected.device)
-    return lengths
-
-
 def default_segments(logits: torch.Tensor) -> int:
     """Split each row so that the grid has about ``BLOCKS_PER_SM`` workgroups per CU, with at
     least ``MIN_SEGMENT`` logits per segment (reference `cuda/sampling.py:43-47`)."""
@@ -50,24 +44,26 @@ def default_segments(logits: torch.Tensor) -> int:
 
 
 def sampling_check(
-    logits: torch.Tensor, selected: torch.Tensor, lengths: torch.Tensor, k: int, top_p: bool,
-    p: float, temperature: float, slack: float, segments: int,
+    logits: torch.Tensor, selected: torch.Tensor, lengths: torch.Tensor | None, k: int,
+    top_p: bool, p: float, temperature: float, slack: float, segments: int,
 ) -> list[torch.Tensor]:  # fmt: skip
     """The pybind ``sampling_check`` of the reference (`bindings.cpp:260-298`): the same
     validation, in the same order and with the same messages; returns
     [passed, min_selected, max_rejected, mass, mass_without_smallest], enqueued on the
-    current stream."""
+    current stream.  ``lengths`` None means every row's selection is its whole width (the
+    reference's top-k call passes a tensor filled with k; here no such tensor is built)."""
     if not logits.is_cuda:
         raise RuntimeError("logits must be a CUDA tensor")
     device = logits.device
     _check_tensor(logits, "logits", torch.float32, device)
     _check_tensor(selected, "selected", torch.int64, device)
-    _check_tensor(lengths, "lengths", torch.int64, device)
-    if not (logits.dim() == 2 and selected.dim() == 2 and lengths.dim() == 1):
+    if lengths is not None:
+        _check_tensor(lengths, "lengths", torch.int64, device)
+    if not (logits.dim() == 2 and selected.dim() == 2 and (lengths is None or lengths.dim() == 1)):
         raise RuntimeError("expected logits (B, V), selected (B, L), lengths (B,)")
     rows, vocab = logits.shape
     max_len = selected.size(1)
-    if not (selected.size(0) == rows and lengths.size(0) == rows):
+    if not (selected.size(0) == rows and (lengths is None or lengths.size(0) == rows)):
         raise RuntimeError("batch sizes differ")
     if not (rows >= 1 and vocab >= 1 and max_len >= 1):
         raise RuntimeError("empty input")
@@ -84,15 +80,20 @@ def sampling_check(
         scratch_ptr = scratch.data_ptr()
     else:
         scratch_ptr = 0
-    partials = torch.empty(rows * segments * handle.pck_sampling_partial_bytes(), dtype=torch.uint8, device=device)
-    passed = torch.empty(rows, dtype=torch.bool, device=device)
-    min_sel = torch.empty(rows, dtype=torch.float32, device=device)
-    max_rej = torch.empty(rows, dtype=torch.float32, device=device)
-    mass = torch.empty(rows, dtype=torch.float64, device=device)
-    without = torch.empty(rows, dtype=torch.float64, device=device)
+    # one allocation for the partials and the five outputs, each at an offset aligned for its
+    # type: [partials | mass | without | min_selected | max_rejected | passed]
+    part = rows * segments * handle.pck_sampling_partial_bytes()  # a multiple of 8
+    buf = torch.empty(part + 25 * rows, dtype=torch.uint8, device=device)
+    partials = buf[:part]
+    mass = buf[part : part + 8 * rows].view(torch.float64)
+    without = buf[part + 8 * rows : part + 16 * rows].view(torch.float64)
+    min_sel = buf[part + 16 * rows : part + 20 * rows].view(torch.float32)
+    max_rej = buf[part + 20 * rows : part + 24 * rows].view(torch.float32)
+    passed = buf[part + 24 * rows : part + 25 * rows].view(torch.bool)
     with torch.cuda.device(device):
         err = handle.pck_sampling_check(
-            logits.data_ptr(), selected.data_ptr(), lengths.data_ptr(), rows, vocab, max_len, k,
+            logits.data_ptr(), selected.data_ptr(), None if lengths is None else lengths.data_ptr(),
+            rows, vocab, max_len, k,
             int(top_p), p, temperature, slack, segments, scratch_ptr, partials.data_ptr(),
             passed.data_ptr(), min_sel.data_ptr(), max_rej.data_ptr(), mass.data_ptr(),
             without.data_ptr(), stream_handle(device),
@@ -107,7 +108,7 @@ def check_topk_gpu(
     """Check that each row of ``selected`` (B, k) is a valid top-k set of ``logits`` (B, V)
     (reference `cuda/sampling.py:50-58`)."""
     segs = default_segments(logits) if segments is None else segments
-    out = sampling_check(logits, selected, _lengths(selected, None), k, False, 1.0, 1.0, 0.0, segs)
+    out = sampling_check(logits, selected, None, k, False, 1.0, 1.0, 0.0, segs)
     return SamplingCheck(*out)
 
 
