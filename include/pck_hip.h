@@ -203,7 +203,7 @@ int pck_batch_check(const PckBatchCheckDesc* descs, int count, void* workspace,
  * kernel behind pck.member.check_members (reference src/pck/member.py:118-197).
  *   logits (rows, vocab) FP32, 1 <= vocab < 2^31; tokens (rows,) int64 (any value:
  *   out-of-range ids reject);
- *   top_k (rows,) int64 or NULL (already clamped to [1, vocab]; vocab = no top-k);
+ *   top_k (rows,) int64 or NULL (clamped to [1, vocab] here; vocab = no top-k);
  *   top_p (rows,) FP64 or NULL (1 = no top-p); greedy (rows,) uint8 or NULL;
  *   slack = next_up(tol + member_eps32(vocab)) from the host;
  *   k_lim = largest host-side top-k below vocab (0 if none); all_k = every host top-k < vocab;

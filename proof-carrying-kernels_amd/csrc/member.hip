@@ -311,7 +311,9 @@ __global__ void __launch_bounds__(kThreads) member_kernel(const MemberArgs A) {
   const int64_t token = A.tokens[r];
   const bool in_range = token >= 0 && token < vocab;
   const float lt = row[in_range ? token : (token < 0 ? 0 : vocab - 1)];
-  const int64_t k_row = A.top_k ? A.top_k[r] : vocab;
+  // a requested top-k is clamped to [1, vocab] (reference src/pck/member.py:153)
+  const int64_t k_req = A.top_k ? A.top_k[r] : vocab;
+  const int64_t k_row = k_req < 1 ? 1 : (k_req > vocab ? vocab : k_req);
   const bool greedy = A.greedy ? A.greedy[r] != 0 : false;
   const double p = A.top_p ? A.top_p[r] : 1.0;
 

@@ -86,18 +86,20 @@ def check_members(
     t = tokens.reshape(rows).to(device=device, dtype=torch.long).contiguous()
     k_dev = None
     k_lim, all_k = 0, False
-    if top_k is not None:
-        k_dev = top_k.to(device=device, dtype=torch.long).reshape(rows).clamp(1, vocab).contiguous()
+    if top_k is not None:  # clamped to [1, V] by the kernel
+        k_dev = top_k.to(device=device, dtype=torch.long).reshape(rows).contiguous()
         k_lim, all_k = _host_top_k(top_k, top_k_host, vocab)
     p_dev = None
     if top_p is not None:
         p_dev = top_p.to(device=device, dtype=torch.float64).reshape(rows).contiguous()
     g_dev = None
-    if greedy is not None:
-        g_dev = greedy.to(device=device, dtype=torch.bool).reshape(rows).to(torch.uint8)
-    ok = torch.empty(rows, dtype=torch.bool, device=device)
-    above = torch.empty(rows, dtype=torch.int64, device=device)
-    mass_above = torch.empty(rows, dtype=torch.float64, device=device)
+    if greedy is not None:  # a bool tensor is read as its bytes (0 or 1)
+        g_dev = greedy.to(device=device, dtype=torch.bool).reshape(rows).contiguous().view(torch.uint8)
+    # the three outputs in one allocation: [mass_above | above | ok]
+    out = torch.empty(17 * rows, dtype=torch.uint8, device=device)
+    mass_above = out[: 8 * rows].view(torch.float64)
+    above = out[8 * rows : 16 * rows].view(torch.int64)
+    ok = out[16 * rows :].view(torch.bool)
     if rows == 0:
         return {"ok": ok, "above": above, "mass_above": mass_above}
     slack = next_up(tol + member_eps32(vocab))

@@ -175,3 +175,21 @@ def test_baseline_workload_flags_every_planted_token() -> None:
         ref = check_member(logits[i], int(tokens[i]), 50, 0.9)
         if ref.ok:
             assert abs(float(out["mass_above"][i]) - ref.mass_above) <= member_eps32(vocab)
+
+
+def test_top_k_outside_one_to_vocab_is_clamped_like_the_reference() -> None:
+    """Requested top-k values below 1 or above V act as 1 and V (reference
+    src/pck/member.py:153); the kernel clamps them, so no host-side clamp launch is needed."""
+    rng = np.random.default_rng(3)
+    logits = (rng.standard_normal((6, 300)) * 3).astype(np.float32)
+    order = np.argsort(-logits, axis=1)
+    tokens = order[np.arange(6), [0, 1, 0, 5, 2, 299]]
+    top_k = np.array([0, -3, 1, 10**9, 301, 300])
+    clamped = np.clip(top_k, 1, 300)
+    got = run(logits, tokens, top_k, np.full(6, 0.9), top_k_host=clamped)
+    want = run(logits, tokens, clamped, np.full(6, 0.9), top_k_host=clamped)
+    for key in ("ok", "above"):
+        np.testing.assert_array_equal(got[key], want[key])
+    # candidates meet in LDS in arrival order, so the FP64 sums may differ in their last bits
+    assert np.all(np.abs(got["mass_above"] - want["mass_above"]) <= 2 * member_eps32(300))
+    assert_matches_oracle(logits, tokens, clamped, np.full(6, 0.9), top_k_host=clamped)
