@@ -1,6 +1,7 @@
 """The reference's low-level extension object (`src/pck/cuda/_ext.py`): ``extension()`` returns
 the native entry points under the names the reference's pybind module exports
-(`src/pck/cuda/csrc/bindings.cpp:302-335`), here bound to libpck_hip.so."""
+(`src/pck/cuda/csrc/bindings.cpp:302-335`), here bound to libpck_hip.so.  The agent-template
+kernels (`gemv_template`, `gemv_template_q8`, `gemv_column`) are not part of this build."""
 
 from __future__ import annotations
 
@@ -14,6 +15,7 @@ from pck.cuda._lib import lib
 def extension() -> SimpleNamespace:
     from pck.cuda import gemv
     from pck.cuda.checker import blocked_check
+    from pck.cuda.sampling import sampling_check
 
     lib()  # fail here, loudly, if the library is not built
     return SimpleNamespace(
@@ -21,4 +23,5 @@ def extension() -> SimpleNamespace:
         gemv_coalesced=lambda W, x, threads: gemv.gemv_coalesced(W, x, threads),
         gemv_fp8=lambda Q, x, threads: gemv.gemv_fp8(Q, x, threads),
         blocked_check=blocked_check,
+        sampling_check=sampling_check,
     )

@@ -218,3 +218,18 @@ def test_short_and_long_nuclei_in_one_call_match_cpu() -> None:
     assert cpu == [True, False, True, True, False, False]
     honest = check_topp_gpu(lg, selected, lengths, 0.9, tol=1e-5)
     assert honest.passed.all()
+
+
+def test_extension_exposes_the_pybind_sampling_check() -> None:
+    """`pck.cuda._ext.extension().sampling_check` takes the reference's pybind arguments
+    (bindings.cpp:331-334) and returns its five outputs."""
+    from pck.cuda._ext import extension
+
+    lg = logits(2, 1000, seed=40)
+    sel, _ = topk_sample(lg, 10)
+    lengths = torch.full((2,), 10, dtype=torch.int64, device="cuda")
+    out = extension().sampling_check(lg, sel, lengths, 10, False, 1.0, 1.0, 0.0, 1)
+    ref = check_topk_gpu(lg, sel, 10, segments=1)
+    assert len(out) == 5 and bool(out[0].all())
+    assert torch.equal(out[0], ref.passed) and torch.equal(out[1], ref.min_selected)
+    assert torch.equal(out[2], ref.max_rejected)
