@@ -24,7 +24,16 @@ ROOT = PACKAGE.parent
 CSRC = ROOT / "csrc"
 INCLUDE = ROOT.parent / "include"
 LIBRARY = PACKAGE / "libpck_hip.so"
-SOURCES = ("gemv.hip", "bgemm.hip", "checker.hip", "bcheck.hip", "member.hip", "sampling.hip", "measure.hip")
+SOURCES = (
+    "gemv.hip",
+    "bgemm.hip",
+    "checker.hip",
+    "bcheck.hip",
+    "member.hip",
+    "sampling.hip",
+    "measure.hip",
+    "template.hip",  # the agent's templates: kernels under test, outside the trusted set
+)
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

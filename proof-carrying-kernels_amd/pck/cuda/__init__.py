@@ -30,6 +30,7 @@ from pck.cuda.gemv import (
     gemv_naive,
     quantize_fp8,
 )
+from pck.cuda.template import column_tiles, gemv_column, gemv_template, row_q8, template_flags
 
 __all__ = [
     "DEFAULT_BLOCK",
@@ -57,4 +58,9 @@ __all__ = [
     "sharded_topk_gpu",
     "topk_sample",
     "topp_select",
+    "column_tiles",
+    "gemv_column",
+    "gemv_template",
+    "row_q8",
+    "template_flags",
 ]

@@ -15,11 +15,16 @@ from pck.cuda import _lib
 
 ROOT = Path(__file__).resolve().parent.parent
 HEADER = ROOT / "include" / "pck_hip.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 
 
 def declared_functions() -> list[str]:
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(pck_\w+)\s*\(", text, flags=re.M)))
+    """Every pck_* function that a header under include/ declares."""
+    names: set[str] = set()
+    for header in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names |= set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(pck_\w+)\s*\(", text, flags=re.M))
+    return sorted(names)
 
 
 def test_header_declares_the_entry_points() -> None:
@@ -34,6 +39,11 @@ def test_header_declares_the_entry_points() -> None:
         "pck_sampling_check",
         "pck_sampling_scratch_words",
         "pck_error_string",
+        "pck_gemv_template",
+        "pck_gemv_template_q8",
+        "pck_gemv_column",
+        "pck_column_tiles",
+        "pck_quantize_rows_q8",
     ):
         assert expected in names
 
@@ -43,6 +53,31 @@ def test_library_exports_every_declared_function() -> None:
     for name in declared_functions():
         assert hasattr(handle, name), name
     assert set(declared_functions()) >= set(_lib.SIGNATURES) | set(_lib.SIZE_QUERIES)
+    from pck.cuda import template
+
+    assert set(declared_functions()) >= set(template.SIGNATURES) | {"pck_column_tiles"}
+
+
+def test_template_header_compiles_as_c_and_argument_counts_match(tmp_path: Path) -> None:
+    """The template header is plain C, and each ctypes signature has the prototype's arity."""
+    from pck.cuda import template
+
+    src = tmp_path / "t.c"
+    src.write_text('#include "pck_template.h"\nint main(void) { return 0; }\n')
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", f"-I{HEADER.parent}", str(src), "-o",
+                    str(tmp_path / "t")], check=True)
+    text = re.sub(r"/\*.*?\*/", "", (HEADER.parent / "pck_template.h").read_text(), flags=re.S)
+    for name, argtypes in template.SIGNATURES.items():
+        params = re.search(name + r"\s*\(([^)]*)\)", text, flags=re.S)
+        assert params is not None, name
+        assert len(params.group(1).split(",")) == len(argtypes), name
+
+
+def test_column_tiles_without_a_gpu() -> None:
+    from pck.cuda.template import column_tiles
+
+    assert column_tiles(0, 8) == 0 and column_tiles(1, 8) == 1 and column_tiles(256, 8) == 1
+    assert column_tiles(257 * 2, 2) == 9 and column_tiles(64, 3) == -1
 
 
 def test_error_strings() -> None:
