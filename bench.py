@@ -29,11 +29,12 @@ Printed JSON line:
                  checker) timed on this host on a bounded sample, one core (the all-core C
                  model in cpu_baseline_all_cores, the FP8 layer in fp8.cpu_baseline)
 plus the FP8 layer, GEMV-only times, the checker overhead, the membership check (256 x 151936
-logits), the set-sampling checker, the batched layer (B = 128, 256) and the read-only stream
+logits), the set-sampling checker, the batched layer (B = 128, 256), the agent's GEMV templates
+over the same layer (row-major, INT8 and column-major configs) and the read-only stream
 ceilings: the long stream (hbm_read_ceiling_gbps) and one launch over each GEMV launch's bytes
 (size_matched_read_us; pct_of_size_matched_read is their sum over the layer's time).
 
-Run: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--quick]
+Run: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--quick] [--section templates]
 """
 
 from __future__ import annotations
@@ -596,6 +597,90 @@ def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: in
     return out
 
 
+def templates_layer(copies: int = 4, depth: int = 32, reps: int = 7) -> dict:
+    """The agent's GEMV templates over the Llama-3-8B decode layer at batch 1: the seven
+    projections as seven launches (a column-major launch with grid splits adds its merge
+    launch), 32-layer passes over ``copies`` layer copies replayed from a HIP graph.  Per config:
+    us per layer, algorithmic GB/s (weights + x + y, plus the scales for INT8) and the share of
+    a size-matched read (one read launch of each projection's bytes).  The default row-major
+    config is the coalesced tree at T = 256 and must equal the trusted gemv_coalesced bit for bit
+    (checked here before timing)."""
+    import torch
+
+    from pck.agent.column import ColumnConfig
+    from pck.agent.config import KernelConfig
+    from pck.cuda import gemv_coalesced, gemv_column, gemv_template, row_q8
+    from pck.cuda.timing import read_stream_ms
+
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    layers = []
+    for _ in range(copies):
+        layer = {}
+        for name, m, n in LAYER:
+            W = (torch.randn(m, n, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+            x = torch.randn(n, device="cuda", generator=gen).to(torch.bfloat16)
+            layer[name] = (W, x, W.t().contiguous(), row_q8(W))
+        layers.append(layer)
+    W, x = layers[0]["down"][:2]
+    assert torch.equal(gemv_template(W, x, KernelConfig()), gemv_coalesced(W, x, 256))
+
+    def q8_bytes(m: int, n: int) -> int:
+        return gemv_bytes(m, n, 1) + 4 * m * (-(-n // 128))
+
+    sizes = {"bf16": [gemv_bytes(m, n, 2) for _, m, n in LAYER],
+             "int8": [q8_bytes(m, n) for _, m, n in LAYER]}  # fmt: skip
+    matched = {k: sum(read_stream_ms(v)) for k, v in sizes.items()}
+    configs = {
+        "row_default": KernelConfig(),
+        "row_t256_v8_u2": KernelConfig(unroll=2),
+        "row_t512_r2_v4_u4": KernelConfig(threads=512, rows_per_block=2, vec=4, unroll=4),
+        "int8_t256_r4_v16": KernelConfig(threads=256, rows_per_block=4, vec=16, weights="int8"),
+        "column_default": ColumnConfig(),
+        "column_t256_v4_s32": ColumnConfig(threads=256, vec=4, splits=32),
+        "column_t128_v8_s1": ColumnConfig(splits=1),
+    }
+
+    def run(cfg, layer):  # type: ignore[no-untyped-def]
+        for name, _, _ in LAYER:
+            W, x, WT, q8 = layer[name]
+            if isinstance(cfg, ColumnConfig):
+                gemv_column(WT, x, cfg)
+            else:
+                gemv_template(W, x, cfg, q8 if cfg.weights == "int8" else None)
+
+    out = {"workload": "Llama-3-8B decode layer, batch 1, 7 launches (+ merges), 32-layer graph passes",
+           "size_matched_read_us": {k: round(1e3 * v, 2) for k, v in matched.items()}}  # fmt: skip
+    for key, cfg in configs.items():
+        run(cfg, layers[0])
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(depth):
+                run(cfg, layers[i % copies])
+        graph.replay()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(reps):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            graph.replay()
+            end.record()
+            end.synchronize()
+            times.append(start.elapsed_time(end) / depth)
+        ms = statistics.median(times)
+        kind = "int8" if getattr(cfg, "weights", "bf16") == "int8" else "bf16"
+        out[key] = {
+            "config": {k: v for k, v in vars(cfg).items() if k != "layout"},
+            "us_per_layer": round(1e3 * ms, 2),
+            "gbps": round(sum(sizes[kind]) / (ms / 1e3) / 1e9, 1),
+            "pct_of_size_matched_read": round(100 * matched[kind] / ms, 2),
+        }
+        del graph
+    del layers
+    torch.cuda.empty_cache()
+    return out
+
+
 def host_cpu() -> str:
     """The host CPU's model name, as /proc/cpuinfo gives it."""
     try:
@@ -671,6 +756,10 @@ def main() -> None:
         "--quick", action="store_true",
         help="one pass per mode, no eager timing, no CPU baseline (for counter collection)",
     )  # fmt: skip
+    parser.add_argument(
+        "--section", choices=("all", "templates"), default="all",
+        help="templates: time only the agent's GEMV templates and print that section",
+    )  # fmt: skip
     args = parser.parse_args()
     if args.quick:
         args.steps, args.warmup, args.no_cpu_baseline = 32, 1, True
@@ -683,6 +772,9 @@ def main() -> None:
 
     from pck.cuda.timing import read_bandwidth_gbps, read_stream_ms
 
+    if args.section == "templates":
+        print(json.dumps({"templates": templates_layer()}), flush=True)
+        return
     bytes_bf16 = sum(gemv_bytes(m, n, 2) for _, m, n in LAYER)
     launch_bytes = {
         launch: sum(gemv_bytes(m, n, 2) for name, m, n in LAYER if name in names)
@@ -753,6 +845,8 @@ def main() -> None:
     sampling = sampling_checker(50 if args.quick else 200)
     print("[bench] timing the batched layer (B = 128, 256)", file=sys.stderr, flush=True)
     batched = batched_layer()
+    print("[bench] timing the agent's GEMV templates", file=sys.stderr, flush=True)
+    templates = templates_layer()
     achieved = dom_bytes / (dom_ms / 1e3) / 1e9
     value = bytes_bf16 / (ms_checked / 1e3) / 1e9
 
@@ -804,6 +898,7 @@ def main() -> None:
         "membership": member,
         "sampling": sampling,
         "batched": batched,
+        "templates": templates,
         "roofline": {
             "bound": "hbm",
             "kernel": "gemv_tree_kernel<256,1,2,bf16,nt> (q/k/v, o, gate/up launches)",

@@ -45,8 +45,9 @@ int64_t pck_column_tiles(int64_t m, int vec);
 /* Column-major template, y = W x from WT = W^T, (n, m) BF16, 16-byte aligned, m % vec == 0.
  * threads = 32 K with K a power of two <= 8; vec in {2, 4, 8}; splits a power of two <= 64;
  * skip_below >= 0 skips (and never reads) every column with |x_j| < skip_below.  With
- * splits > 1: scratch holds splits * m floats and tickets pck_column_tiles(m, vec) zeros, which
- * the call leaves zero, so calls that share tickets must not overlap (one stream per device).
+ * splits > 1, scratch holds splits * m floats and a second launch on `stream` merges them, so
+ * calls may overlap when their scratch buffers differ.  `tickets` is not read (the reference
+ * merges through zeroed tickets; here the merge is a launch of its own) and may be NULL.
  * Replaces pck::gemv_column, reference src/pck/cuda/csrc/column_kernel.cu:154-184 (bound at
  * src/pck/cuda/csrc/bindings.cpp:127-151). */
 int pck_gemv_column(const void* WT, const void* x, float* y, float* scratch, unsigned* tickets,

@@ -24,12 +24,14 @@
 // splits); a workgroup of K = threads / 32 virtual warps, lane g of warp k owning rows
 // r0 .. r0 + VEC - 1 of the tile.  Grid split s owns the contiguous columns [s C, (s + 1) C),
 // C = ceil(n / splits), and warp k sums columns s C + k, s C + k + K, ... from +0.  The K sums are
-// halved in LDS.  With splits > 1 each workgroup stores its sums, and the last workgroup of a
-// row tile to take the tile's ticket halves the splits in a fixed order and clears the ticket.
-// Partials are published with an agent-scope release and read after an agent-scope acquire:
-// MI355X's XCDs have separate L2 caches.  With skip_below > 0 (the activation-sparsity exploit)
-// a column with |x_j| < skip_below is not read at all; the test is the same for the 32 lanes of
-// a virtual warp, so the whole 32 VEC-value load is skipped.
+// halved in LDS.  With splits > 1 each workgroup stores its sum for each row, and a second launch
+// halves each row's `splits` sums in a fixed order.  The reference merges in the last workgroup
+// of a row tile through an atomic ticket; on MI355X that needs an agent-scope release and acquire
+// around every ticket (each XCD has its own L2, which the fences write back and invalidate), and
+// those fences made the Llama-3-8B layer about 4x slower than the second launch does.  With
+// skip_below > 0 (the activation-sparsity exploit) a column with |x_j| < skip_below is not read
+// at all; the test is the same for the 32 lanes of a virtual warp, so the whole 32 VEC-value load
+// is skipped.
 //
 // INT8 copy (reference src/pck/agent/config.py:163-175, NumPy on the CPU there): one wave per
 // (row, 128-column group) finds max |w|, scale = max / 127 (1 for an all-zero group) and
@@ -310,14 +312,16 @@ hipError_t launch_row(bool q8, const void* W, const float* S, const void* x, flo
 
 constexpr int kColMaxWarps = 8;
 constexpr int kColMaxSplits = 64;
-constexpr int kColAhead = 4;  // columns loaded before their terms are added (order unchanged)
+// Columns loaded before their terms are added (the order is unchanged).  8 measured faster than
+// 4 on the Llama-3-8B layer; 16 spills registers.
+constexpr int kColAhead = 8;
+constexpr int kMergeThreads = 256;
 
 struct ColumnArgs {
   const uint16_t* WT;  // (n, m) BF16
   const uint16_t* x;   // (n,) BF16
   float* y;            // (m,)
   float* scratch;      // (splits, m) when splits > 1
-  unsigned* tickets;   // one per row tile, zero between calls
   int64_t m;
   int64_t n;
   int64_t chunk;  // C = ceil(n / splits)
@@ -329,12 +333,9 @@ __device__ __forceinline__ void load_row_vec(const uint16_t* p, uint32_t (&w)[VE
   load_words<2 * VEC>(reinterpret_cast<const unsigned char*>(p), w);
 }
 
-// At most 64 VGPRs (8 waves per SIMD), so that many column loads are in flight.
 template <int VEC, bool kSkip>
-__global__ void __launch_bounds__(kWarp* kColMaxWarps) __attribute__((amdgpu_waves_per_eu(8)))
-column_template_kernel(const ColumnArgs a) {
+__global__ void __launch_bounds__(kWarp* kColMaxWarps) column_template_kernel(const ColumnArgs a) {
   __shared__ float part[kColMaxWarps][VEC][kWarp];
-  __shared__ int is_last;
   const int k = static_cast<int>(threadIdx.x) / kWarp;
   const int g = static_cast<int>(threadIdx.x) % kWarp;
   const int warps = static_cast<int>(blockDim.x) / kWarp;
@@ -402,35 +403,23 @@ column_template_kernel(const ColumnArgs a) {
     for (int v = 0; v < VEC; ++v)
       a.scratch[static_cast<int64_t>(blockIdx.y) * a.m + r0 + v] = part[0][v][g];
   }
-  __threadfence();  // agent-scope release of this lane's partial sums
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __threadfence();
-    const unsigned before = __hip_atomic_fetch_add(&a.tickets[blockIdx.x], 1u, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT);
-    is_last = before == static_cast<unsigned>(splits) - 1;
-  }
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();  // agent-scope acquire: the other workgroups' partial sums are visible
+}
 
-  // The last workgroup of the row tile halves each row's split sums in a fixed order: lane s of a
-  // segment of w = splits / 2 lanes adds sums s and s + w (the first halving step), and the
-  // segment finishes by shuffle-down halving, whose lane 0 holds the halving order's value.
-  const int64_t tile_rows = a.m - tile0 < kWarp * VEC ? a.m - tile0 : kWarp * VEC;
+// Halves each row's `splits` sums (a[i] += a[i + splits / 2], then splits / 4, ...): lane s of a
+// segment of w = splits / 2 lanes adds sums s and s + w (the first step) and the segment
+// finishes by shuffle-down halving, whose lane 0 holds the halving order's value.
+__global__ void __launch_bounds__(kMergeThreads)
+    column_merge_kernel(const float* __restrict__ scratch, float* __restrict__ y, int64_t m,
+                        int splits) {
   const int w = splits / 2;
   const int s = static_cast<int>(threadIdx.x) % w;
-  const int per_pass = static_cast<int>(blockDim.x) / w;
-  for (int64_t base = 0; base < tile_rows; base += per_pass) {  // uniform: every lane shuffles
-    const int64_t i = base + static_cast<int>(threadIdx.x) / w;
-    const int64_t row = tile0 + (i < tile_rows ? i : 0);
-    float v = a.scratch[static_cast<int64_t>(s) * a.m + row] +
-              a.scratch[static_cast<int64_t>(s + w) * a.m + row];
-    for (int off = w / 2; off > 0; off /= 2) v = v + __shfl_down(v, off, w);
-    if (s == 0 && i < tile_rows) a.y[row] = v;
-  }
-  if (threadIdx.x == 0)  // ready for the next call
-    __hip_atomic_store(&a.tickets[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * (kMergeThreads / w) +
+                    static_cast<int>(threadIdx.x) / w;
+  const int64_t row = i < m ? i : 0;  // every lane takes part in the shuffles
+  float v = scratch[static_cast<int64_t>(s) * m + row] +
+            scratch[static_cast<int64_t>(s + w) * m + row];
+  for (int off = w / 2; off > 0; off /= 2) v = v + __shfl_down(v, off, w);
+  if (s == 0 && i < m) y[row] = v;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -494,6 +483,7 @@ int pck_gemv_column(const void* WT, const void* x, float* y, float* scratch, uns
                     int64_t m, int64_t n, int threads, int vec, int splits, float skip_below,
                     void* stream) {
   using namespace pck;
+  (void)tickets;  // the split sums are merged by a second launch, not through tickets
   const int warps = threads / kWarp;
   if (threads < kWarp || threads > kWarp * kColMaxWarps || threads % kWarp != 0 ||
       (warps & (warps - 1)) != 0 || splits < 1 || splits > kColMaxSplits ||
@@ -502,12 +492,14 @@ int pck_gemv_column(const void* WT, const void* x, float* y, float* scratch, uns
     return hipErrorInvalidValue;
   if (m == 0) return hipSuccess;
   if (WT == nullptr || (n > 0 && x == nullptr) || y == nullptr ||
-      (splits > 1 && (scratch == nullptr || tickets == nullptr)))
+      (splits > 1 && scratch == nullptr))
     return hipErrorInvalidValue;
   const int64_t tiles = pck_column_tiles(m, vec);
-  if (tiles > 0x7FFFFFFF) return hipErrorInvalidValue;
+  const int64_t rows_per_merge = splits > 1 ? kMergeThreads / (splits / 2) : 1;
+  const int64_t merge_groups = (m + rows_per_merge - 1) / rows_per_merge;
+  if (tiles > 0x7FFFFFFF || merge_groups > 0x7FFFFFFF) return hipErrorInvalidValue;
   const ColumnArgs a{static_cast<const uint16_t*>(WT), static_cast<const uint16_t*>(x), y, scratch,
-                     tickets, m, n, (n + splits - 1) / splits, skip_below};
+                     m, n, (n + splits - 1) / splits, skip_below};
   const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits));
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const bool skip = skip_below > 0.0f;
@@ -524,6 +516,12 @@ int pck_gemv_column(const void* WT, const void* x, float* y, float* scratch, uns
       skip ? column_template_kernel<8, true><<<grid, threads, 0, s>>>(a)
            : column_template_kernel<8, false><<<grid, threads, 0, s>>>(a);
       break;
+  }
+  if (splits > 1) {
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    column_merge_kernel<<<dim3(static_cast<unsigned>(merge_groups)), dim3(kMergeThreads), 0, s>>>(
+        scratch, y, m, splits);
   }
   return hipGetLastError();
 }

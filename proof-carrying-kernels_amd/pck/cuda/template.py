@@ -4,7 +4,8 @@ libpck_hip.so (`include/pck_template.h`).
 Same names, arguments and error behaviour as the reference: `gemv_template` runs the
 row-major template with a `KernelConfig` (from the INT8 copy ``q8 = (Wq, S)`` when
 ``cfg.weights == "int8"``), `row_q8` makes that copy, and `gemv_column` runs the column-major
-template with a `ColumnConfig` from ``WT = W.t().contiguous()``.  Validation messages follow
+template with a `ColumnConfig` from ``WT = W.t().contiguous()`` (no merge tickets: the grid
+splits are merged by a second launch).  Validation messages follow
 `src/pck/cuda/csrc/bindings.cpp:85-151` (RuntimeError).  Outputs are FP32 on the input's device;
 kernels are enqueued on the current stream without synchronising.
 
@@ -112,23 +113,12 @@ def _template_q8(
     return y
 
 
-_TICKETS: dict[torch.device, torch.Tensor] = {}
-
-
-def _tickets(device: torch.device, count: int) -> torch.Tensor:
-    """Zeroed merge tickets for `gemv_column`, kept per device (each call leaves them zero)."""
-    t = _TICKETS.get(device)
-    if t is None or t.numel() < count:
-        t = torch.zeros(max(count, 1024), dtype=torch.int32, device=device)
-        _TICKETS[device] = t
-    return t
-
-
-def _column(
-    WT: torch.Tensor, x: torch.Tensor, tickets: torch.Tensor, threads: int, vec: int, splits: int,
-    skip_below: float,
+def _column_run(
+    WT: torch.Tensor, x: torch.Tensor, threads: int, vec: int, splits: int, skip_below: float,
+    tickets: torch.Tensor | None = None,
 ) -> torch.Tensor:  # fmt: skip
-    """The column-major template (reference binding `src/pck/cuda/csrc/bindings.cpp:127-151`)."""
+    """The column-major template (reference binding `src/pck/cuda/csrc/bindings.cpp:127-151`);
+    ``tickets`` is only validated, as the reference does, and never read."""
     if not (WT.is_cuda and x.is_cuda and WT.device == x.device):
         raise RuntimeError("WT and x must be CUDA tensors on one device")
     if not (WT.dtype == torch.bfloat16 and x.dtype == torch.bfloat16):
@@ -142,21 +132,30 @@ def _column(
     scratch = torch.empty(splits * m if splits > 1 else 0, dtype=torch.float32, device=WT.device)
     if m == 0:
         return y
-    tiles = column_tiles(m, vec) if vec in (2, 4, 8) else 0
-    if not (
-        vec > 0 and tickets.is_cuda and tickets.device == WT.device
-        and tickets.dtype == torch.int32 and tickets.is_contiguous() and tickets.numel() >= tiles
-    ):  # fmt: skip
-        raise RuntimeError(
-            "tickets must be a zeroed int32 CUDA tensor with at least one entry per tile"
-        )
+    if tickets is not None:
+        tiles = column_tiles(m, vec) if vec in (2, 4, 8) else 0
+        if not (
+            vec > 0 and tickets.is_cuda and tickets.device == WT.device
+            and tickets.dtype == torch.int32 and tickets.is_contiguous() and tickets.numel() >= tiles
+        ):  # fmt: skip
+            raise RuntimeError(
+                "tickets must be a zeroed int32 CUDA tensor with at least one entry per tile"
+            )
     with torch.cuda.device(WT.device):
         err = _lib().pck_gemv_column(
-            WT.data_ptr(), x.data_ptr(), y.data_ptr(), scratch.data_ptr(), tickets.data_ptr(),
-            m, n, threads, vec, splits, skip_below, stream_handle(WT.device),
+            WT.data_ptr(), x.data_ptr(), y.data_ptr(), scratch.data_ptr(), None, m, n, threads,
+            vec, splits, skip_below, stream_handle(WT.device),
         )  # fmt: skip
     check(err, "column gemv launch")
     return y
+
+
+def _column(
+    WT: torch.Tensor, x: torch.Tensor, tickets: torch.Tensor, threads: int, vec: int, splits: int,
+    skip_below: float,
+) -> torch.Tensor:  # fmt: skip
+    """The reference extension's signature, with its merge tickets (validated, not read)."""
+    return _column_run(WT, x, threads, vec, splits, skip_below, tickets)
 
 
 def gemv_template(
@@ -210,10 +209,7 @@ def row_q8(
 def gemv_column(WT: torch.Tensor, x: torch.Tensor, cfg: ColumnConfig) -> torch.Tensor:
     """y = W x with the column-major template, from ``WT = W.t().contiguous()``.
 
-    Bit-identical to the template's CPU model.  Calls on one device share the merge tickets,
-    so they must not overlap: use one stream per device.
+    Bit-identical to the template's CPU model.  The grid splits are merged by a second launch
+    on the same stream (no shared tickets), so calls may overlap on one device.
     """
-    tiles = column_tiles(WT.shape[1], cfg.vec) if WT.dim() == 2 else 0
-    return _column(
-        WT, x, _tickets(WT.device, tiles), cfg.threads, cfg.vec, cfg.splits, cfg.skip_below
-    )
+    return _column_run(WT, x, cfg.threads, cfg.vec, cfg.splits, cfg.skip_below)
