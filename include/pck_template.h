@@ -24,7 +24,7 @@ extern "C" {
  * 2 partials BF16, 4 output BF16, 8 skip the columns past the last full tile of vec * tpr.
  * Vector loads when n % vec == 0 and W, x are aligned to vec elements; the bits are the same
  * either way.  Returns hipErrorInvalidValue for any other knob, m > INT32_MAX or n < 1 (m > 0).
- * Replaces pck::gemv_template, reference src/pck/cuda/csrc/template_kernel.cu:291-297
+ * Replaces pck::gemv_template, reference src/pck/cuda/csrc/template_kernel.cu:293-298
  * (bound at src/pck/cuda/csrc/bindings.cpp:85-96). */
 int pck_gemv_template(const void* W, const void* x, float* y, int64_t m, int64_t n, int threads,
                       int rows_per_block, int vec, int unroll, int flags, void* stream);
@@ -32,14 +32,14 @@ int pck_gemv_template(const void* W, const void* x, float* y, int64_t m, int64_t
 /* The row-major template over an INT8 copy of W: Wq (m, n) int8 and S (m, ceil(n / 128)) FP32
  * (from pck_quantize_rows_q8); the term for column j is fl(fl(q_ij S[i, j / 128]) x_j).  The FP32
  * path (no flags); vec may also be 16.
- * Replaces pck::gemv_template_q8, reference src/pck/cuda/csrc/template_kernel.cu:299-305
+ * Replaces pck::gemv_template_q8, reference src/pck/cuda/csrc/template_kernel.cu:300-306
  * (bound at src/pck/cuda/csrc/bindings.cpp:98-125). */
 int pck_gemv_template_q8(const void* Wq, const float* S, const void* x, float* y, int64_t m,
                          int64_t n, int threads, int rows_per_block, int vec, int unroll,
                          void* stream);
 
 /* Row tiles of the column-major template: ceil(m / (32 vec)); -1 for m < 0 or vec not in
- * {2, 4, 8}.  Replaces pck::column_tiles, reference src/pck/cuda/csrc/column_kernel.cu:152. */
+ * {2, 4, 8}.  Replaces pck::column_tiles, reference src/pck/cuda/csrc/column_kernel.cu:154. */
 int64_t pck_column_tiles(int64_t m, int vec);
 
 /* Column-major template, y = W x from WT = W^T, (n, m) BF16, 16-byte aligned, m % vec == 0.
@@ -48,7 +48,7 @@ int64_t pck_column_tiles(int64_t m, int vec);
  * splits > 1, scratch holds splits * m floats and a second launch on `stream` merges them, so
  * calls may overlap when their scratch buffers differ.  `tickets` is not read (the reference
  * merges through zeroed tickets; here the merge is a launch of its own) and may be NULL.
- * Replaces pck::gemv_column, reference src/pck/cuda/csrc/column_kernel.cu:154-184 (bound at
+ * Replaces pck::gemv_column, reference src/pck/cuda/csrc/column_kernel.cu:158-184 (bound at
  * src/pck/cuda/csrc/bindings.cpp:127-151). */
 int pck_gemv_column(const void* WT, const void* x, float* y, float* scratch, unsigned* tickets,
                     int64_t m, int64_t n, int threads, int vec, int splits, float skip_below,
@@ -59,7 +59,7 @@ int pck_gemv_column(const void* WT, const void* x, float* y, float* scratch, uns
  * one zero-padded): S = max |w| / 127 (1 for an all-zero group), q = round-half-even(w / S)
  * clipped to [-127, 127], divisions correctly rounded.
  * Replaces pck.agent.config.quantize_rows, a NumPy function in the reference
- * (src/pck/agent/config.py:163-175) called by src/pck/cuda/gemv.py:101-109. */
+ * (src/pck/agent/config.py:163-175) called by src/pck/cuda/gemv.py:95-102. */
 int pck_quantize_rows_q8(const void* W, int w_kind, int8_t* Wq, float* S, int64_t m, int64_t n,
                          void* stream);
 

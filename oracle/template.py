@@ -1,7 +1,7 @@
 """TEST INFRASTRUCTURE — bit-exact CPU models of the agent's GEMV templates.
 
 Restates `src/pck/agent/config.py:163-219` (the INT8 copy and the row-major model) and
-`src/pck/agent/column.py:84-106` (the column-major model) of proof-carrying-kernels.  The HIP
+`src/pck/agent/column.py:87-106` (the column-major model) of proof-carrying-kernels.  The HIP
 kernels in `proof-carrying-kernels_amd/csrc/template.hip` must match these models bit for bit.
 NumPy FP32 arithmetic rounds to nearest and keeps subnormals, so each model is an exact IEEE
 restatement of its summation order.
@@ -11,11 +11,12 @@ How each model is pinned (tests/test_oracle_template.py):
     C model and the reference's golden vectors pin; rows_per_block and unroll change nothing;
     every exploit knob is checked against a closed form (BF16 output = bf16 of the honest
     output, skip_tail = the honest model on W with the tail zeroed, BF16 partials = halving of
-    the BF16-rounded chain sums) and the honest variants against the proven bound
-    gamma_h * sum |w x| for the height the config reports;
+    the BF16-rounded chain sums, BF16 accumulator on two-term chains = bf16(p_t + p_{t+32})
+    with the first term unrounded), small-integer sums are exact, and the honest variants
+    meet the proven bound gamma_h * sum |w x| for the height the config reports;
   - `emulate_column` against an explicit per-column loop over the reference's own worked
-    layout (`tests/agent/test_config.py:112-126`), against exact integer sums, and against the
-    bound;
+    layout (`tests/agent/test_config.py:111-125`), against exact integer sums, against
+    skipping = zeroing the skipped activations, and against the bound;
   - `quantize_rows` against its definition on hand-made groups (ties to even, an all-zero
     group, the +-127 clip, partial last groups).
 """
@@ -100,7 +101,7 @@ def emulate_column(
     cfg: ColumnConfig, W: NDArray[np.float32], x: NDArray[np.float32]
 ) -> NDArray[np.float32]:
     """y = W x in the order of the column-major template (reference
-    `src/pck/agent/column.py:84-106`).
+    `src/pck/agent/column.py:87-106`).
 
     Grid split s owns columns [s C, (s + 1) C), C = ceil(n / splits); workgroup split k of the
     K = threads / 32 sums columns s C + k + K i for i = 0, 1, ... from +0 (skipped columns and

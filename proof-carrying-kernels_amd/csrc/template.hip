@@ -1,10 +1,10 @@
 // The agent's GEMV templates on gfx950: the row-major template (BF16 or INT8 weights, exploit
-// knobs), the column-major template over W^T, and the INT8 weight copy they read.
+// knobs) and the column-major template over W^T.  The INT8 weight copy is made in quantize.hip.
 //
 // These are the kernels under test, not part of the trusted set: they share no code with the
 // trusted GEMV tree or the checkers, so editing them cannot change what the checker pin covers.
 //
-// Row-major template (reference src/pck/cuda/csrc/template_kernel.cu:113-174, model
+// Row-major template (reference src/pck/cuda/csrc/template_kernel.cu:114-174, model
 // src/pck/agent/config.py:194-219).  A workgroup of `threads` lanes computes rows_per_block
 // rows; row g of the workgroup is lanes [g tpr, (g + 1) tpr), tpr = threads / rows_per_block, a
 // power-of-two multiple of 32, so every 32-lane virtual warp is one half of a 64-lane wave.  Lane
@@ -19,8 +19,8 @@
 // BF16, 8 drop the columns past the last full tile of VEC tpr columns.  The INT8 variant reads
 // Wq (m, n) and S (m, ceil(n / 128)) and adds fl(fl(q s) x_j), FP32 path only.
 //
-// Column-major template (reference src/pck/cuda/csrc/column_kernel.cu:51-134, model
-// src/pck/agent/column.py:84-106).  WT = W^T is (n, m).  Grid (row tiles of 32 VEC rows,
+// Column-major template (reference src/pck/cuda/csrc/column_kernel.cu:52-141, model
+// src/pck/agent/column.py:87-106).  WT = W^T is (n, m).  Grid (row tiles of 32 VEC rows,
 // splits); a workgroup of K = threads / 32 virtual warps, lane g of warp k owning rows
 // r0 .. r0 + VEC - 1 of the tile.  Grid split s owns the contiguous columns [s C, (s + 1) C),
 // C = ceil(n / splits), and warp k sums columns s C + k, s C + k + K, ... from +0.  The K sums are
@@ -33,10 +33,6 @@
 // at all; the test is the same for the 32 lanes of a virtual warp, so the whole 32 VEC-value load
 // is skipped.
 //
-// INT8 copy (reference src/pck/agent/config.py:163-175, NumPy on the CPU there): one wave per
-// (row, 128-column group) finds max |w|, scale = max / 127 (1 for an all-zero group) and
-// q = round-half-even(w / scale) clipped to [-127, 127], with correctly rounded divisions.
-
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -422,39 +418,6 @@ __global__ void __launch_bounds__(kMergeThreads)
   if (s == 0 && i < m) y[row] = v;
 }
 
-// ---------------------------------------------------------------------------------------------
-// INT8 copy: one wave per (row, group), two columns per lane.
-
-template <bool kF32>
-__global__ void __launch_bounds__(256)
-    quantize_rows_kernel(const void* __restrict__ W, int8_t* __restrict__ Wq,
-                         float* __restrict__ S, int64_t m, int64_t n, int64_t groups) {
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * (256 / kWave) + threadIdx.x / kWave;
-  if (item >= m * groups) return;  // uniform per wave
-  const int lane = static_cast<int>(threadIdx.x) % kWave;
-  const int64_t row = item / groups;
-  const int64_t c0 = (item % groups) * kQ8Group + 2 * lane;
-  float w[2];
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int64_t c = c0 + e;
-    const int64_t at = row * n + (c < n ? c : 0);
-    const float v = kF32 ? static_cast<const float*>(W)[at]
-                         : bf16_bits(static_cast<const uint16_t*>(W)[at]);
-    w[e] = c < n ? v : 0.0f;  // the padded tail of the last group is zero
-  }
-  float amax = fmaxf(fabsf(w[0]), fabsf(w[1]));
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off /= 2) amax = fmaxf(amax, __shfl_xor(amax, off));
-  const float scale = amax > 0.0f ? __fdiv_rn(amax, 127.0f) : 1.0f;
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const float q = fminf(fmaxf(rintf(__fdiv_rn(w[e], scale)), -127.0f), 127.0f);
-    if (c0 + e < n) Wq[row * n + c0 + e] = static_cast<int8_t>(q);
-  }
-  if (lane == 0) S[item] = scale;
-}
-
 }  // namespace
 }  // namespace pck
 
@@ -522,26 +485,6 @@ int pck_gemv_column(const void* WT, const void* x, float* y, float* scratch, uns
     if (err != hipSuccess) return err;
     column_merge_kernel<<<dim3(static_cast<unsigned>(merge_groups)), dim3(kMergeThreads), 0, s>>>(
         scratch, y, m, splits);
-  }
-  return hipGetLastError();
-}
-
-int pck_quantize_rows_q8(const void* W, int w_kind, int8_t* Wq, float* S, int64_t m, int64_t n,
-                         void* stream) {
-  using namespace pck;
-  if ((w_kind != 0 && w_kind != 1) || m < 0 || n < 0 || m > 0x7FFFFFFF) return hipErrorInvalidValue;
-  if (m == 0 || n == 0) return hipSuccess;
-  if (W == nullptr || Wq == nullptr || S == nullptr) return hipErrorInvalidValue;
-  const int64_t groups = (n + kQ8Group - 1) / kQ8Group;
-  const int64_t blocks = (m * groups + 3) / 4;
-  if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  if (w_kind == 1) {
-    quantize_rows_kernel<true><<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s>>>(
-        W, Wq, S, m, n, groups);
-  } else {
-    quantize_rows_kernel<false><<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s>>>(
-        W, Wq, S, m, n, groups);
   }
   return hipGetLastError();
 }

@@ -33,6 +33,7 @@ SOURCES = (
     "sampling.hip",
     "measure.hip",
     "template.hip",  # the agent's templates: kernels under test, outside the trusted set
+    "quantize.hip",  # their INT8 weight copy
 )
 ARCH = "gfx950"
 

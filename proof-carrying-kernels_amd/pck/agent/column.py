@@ -1,4 +1,4 @@
-"""Knobs of the column-major GEMV template (reference `src/pck/agent/column.py:28-81`).
+"""Knobs of the column-major GEMV template (reference `src/pck/agent/column.py:31-85`).
 
 W is stored transposed once at weight load (``WT = W^T``, shape (n, m)), so column j of W is
 the contiguous row ``WT[j]``.  A workgroup of ``threads`` lanes is K = threads / 32 column

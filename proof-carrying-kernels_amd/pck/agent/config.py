@@ -1,4 +1,4 @@
-"""Knobs of the row-major GEMV template (reference `src/pck/agent/config.py:33-151`).
+"""Knobs of the row-major GEMV template (reference `src/pck/agent/config.py:43-161`).
 
 The row-major template is the coalesced tree with knobs.  A workgroup of ``threads`` lanes
 computes ``rows_per_block`` rows, so a row gets tpr = threads / rows_per_block lanes (at least
@@ -158,7 +158,7 @@ def int8_space() -> list[KernelConfig]:
 @cache
 def config_space() -> tuple[Config, ...]:
     """Every valid config of both templates in the reference's order: row-major, then
-    column-major, then row-major with INT8 weights (`src/pck/agent/config.py:128-135`)."""
+    column-major, then row-major with INT8 weights (`src/pck/agent/config.py:133-139`)."""
     return (*row_space(), *column_space(), *int8_space())
 
 

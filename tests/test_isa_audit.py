@@ -68,6 +68,11 @@ def test_reciprocals_only_in_their_idioms() -> None:
     ieee_div = kernel("\tv_rcp_f64_e32 v[2:3], v[0:1]\n\tv_fma_f64 v[4:5], v[0:1], v[2:3], 1.0\n\tv_div_fixup_f64 v[6:7], v[4:5], v[0:1], v[8:9]")
     assert audit.violations("sampling.hip", ieee_div) == []
     assert audit.violations("sampling.hip", kernel("\tv_rcp_f64_e32 v[2:3], v[0:1]\n\tv_mul_f64 v[4:5], v[2:3], v[6:7]"))
+    ieee_div32 = kernel("\tv_div_scale_f32 v2, s[0:1], v1, v1, v0\n\tv_rcp_f32_e32 v3, v2\n"
+                        "\tv_fma_f32 v4, -v2, v3, 1.0\n\tv_div_fixup_f32 v5, v4, v1, v0")
+    assert audit.violations("quantize.hip", ieee_div32) == []
+    # the fused refinement of that sequence is still a multiply-add in a tree source
+    assert any("multiply-add" in v for v in audit.violations("template.hip", ieee_div32))
 
 
 def test_build_flags() -> None:
@@ -80,3 +85,11 @@ def test_build_flags() -> None:
 @pytest.mark.skipif(shutil.which("hipcc") is None and not _build.Path("/opt/rocm/bin/hipcc").exists(), reason="needs hipcc")
 def test_the_trusted_builds_pass() -> None:
     assert audit.audit() == []
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None and not _build.Path("/opt/rocm/bin/hipcc").exists(), reason="needs hipcc")
+def test_the_other_library_sources_pass_the_same_rules() -> None:
+    """The agent's templates (bit-exact trees, so no multiply-add), their INT8 copy and the
+    read stream: every source built into the library is audited."""
+    assert set(audit.LIBRARY_HIP) == set(_build.SOURCES)
+    assert audit.audit(audit.OTHER_HIP) == []
