@@ -336,12 +336,18 @@ struct TreeShape {
 
 TreeShape g_shape_override = {0, 0, 0};
 
-// Defaults from a sweep of every shape over the Llama-3-8B decode launches on MI355X
-// (non-temporal weight loads won everywhere; FP8 rows are half as long, so two rows per wave
-// keep as many bytes in flight as one BF16 row).
-TreeShape choose_shape(int64_t per_lane, bool fp8) {
+// Defaults from sweeps of every shape over each Llama-3-8B decode launch on MI355X.  BF16:
+// non-temporal weight loads won everywhere.  FP8 rows are half as long, so two rows per wave
+// keep as many bytes in flight as one BF16 row, except for a launch of at most 4096 rows (o),
+// where one row per wave and two positions ahead give twice the waves (4.9 against 5.4 us);
+// FP8 rows of more than two positions per lane (down) stream faster with plain loads
+// (12.5 against 13.0 us).
+TreeShape choose_shape(int64_t per_lane, int64_t rows, bool fp8) {
   if (g_shape_override.rows > 0) return g_shape_override;
-  if (fp8) return TreeShape{2, 1, 1};
+  if (fp8) {
+    if (per_lane > 2) return TreeShape{2, 1, 0};
+    return rows <= 4096 ? TreeShape{1, 2, 1} : TreeShape{2, 1, 1};
+  }
   return per_lane > 2 ? TreeShape{2, 2, 1} : TreeShape{1, 2, 1};
 }
 
@@ -402,21 +408,26 @@ hipError_t launch_for_threads(GemvBatch& batch, bool vector, bool pad, TreeShape
              : launch_vector<T, kFp8, false>(batch, shape, s);
 }
 
-template <int R, int U, bool kFp8, bool kPad>
+template <int R, int U, bool kFp8, bool kPad, bool kNt = true>
 hipError_t launch_ride_shape(GemvBatch& batch, const PckCheckBatch& ride, hipStream_t stream) {
   const int64_t groups = plan_groups(batch, static_cast<int64_t>(R) * kWavesPerGroup);
   const int64_t total = groups + ride.start[ride.count];
   if (total * kGroupThreads > 0xFFFFFFFFll) return hipErrorInvalidValue;  // 32-bit dispatch size
-  gemv_ride_kernel<256, R, U, kFp8, kPad, true>
+  gemv_ride_kernel<256, R, U, kFp8, kPad, kNt>
       <<<dim3(static_cast<unsigned>(total)), dim3(kGroupThreads), 0, stream>>>(batch, ride);
   return hipGetLastError();
 }
 
-// The carried-check launch uses the built-in shape of the T = 256 vector path.
+// The carried-check launch uses the built-in shape of the T = 256 vector path for long rows
+// (choose_shape's), the launches a layer's checks ride in.
 template <bool kFp8>
 hipError_t launch_ride(GemvBatch& batch, bool pad, int64_t per_lane, const PckCheckBatch& ride,
                        hipStream_t stream) {
   if constexpr (kFp8) {
+    if (per_lane > 2) {
+      return pad ? launch_ride_shape<2, 1, true, true, false>(batch, ride, stream)
+                 : launch_ride_shape<2, 1, true, false, false>(batch, ride, stream);
+    }
     return pad ? launch_ride_shape<2, 1, true, true>(batch, ride, stream)
                : launch_ride_shape<2, 1, true, false>(batch, ride, stream);
   } else {
@@ -468,7 +479,9 @@ hipError_t launch_group(const PckGemv* gemvs, int count, int threads, const PckC
     const int err = pck_blocked_check(ride, stream);
     if (err != 0) return static_cast<hipError_t>(err);
   }
-  const TreeShape shape = choose_shape(max_per_lane, kFp8);
+  int64_t rows = 0;
+  for (int g = 0; g < count; ++g) rows += batch.item[g].m;
+  const TreeShape shape = choose_shape(max_per_lane, rows, kFp8);
   switch (threads) {
     case 32: return launch_for_threads<32, kFp8>(batch, vector, pad, shape, stream);
     case 64: return launch_for_threads<64, kFp8>(batch, vector, pad, shape, stream);
