@@ -245,3 +245,49 @@ def test_extension_exposes_the_template_bindings() -> None:
     assert not tickets.any()
     with pytest.raises(RuntimeError, match="tickets"):
         ext.gemv_column(to_gpu(W.T), xg, torch.zeros(0, dtype=torch.int32, device="cuda"), 64, 2, 4, 0.0)
+
+
+@pytest.mark.parametrize(
+    "cfg",
+    [
+        KernelConfig(),
+        KernelConfig(threads=128, rows_per_block=2, vec=4, unroll=4),
+        ColumnConfig(),
+        KernelConfig(acc="bf16"),
+        KernelConfig(partials="bf16"),
+        KernelConfig(out="bf16"),
+        KernelConfig(threads=64, skip_tail=True),
+        KernelConfig(vec=16, weights="int8"),
+        ColumnConfig(skip_below=0.3),
+    ],
+    ids=str,
+)
+def test_the_trusted_checker_judges_template_outputs_like_the_cpu_checker(cfg) -> None:  # type: ignore[no-untyped-def]
+    """What the templates exist for: their GPU outputs go to the trusted GPU checker at the
+    config's own tree height, and its verdicts equal the CPU checker's on the same signs.
+    Honest configs pass every block; each exploit is rejected."""
+    from oracle.checker import BlockedChecker
+    from pck.agent.config import is_exploit
+    from pck.cuda import GpuBlockedChecker
+
+    m, n = 512, 2000  # n is not a multiple of a 64-lane x 8-column tile: skip_tail drops 464
+    rng = np.random.default_rng(11)
+    W = bf16(rng.standard_normal((m, n)) * 0.02)
+    x = bf16(rng.standard_normal(n))
+    Wg, xg = to_gpu(W), to_gpu(x)
+    if isinstance(cfg, ColumnConfig):
+        y = gemv_column(to_gpu(W.T), xg, cfg)
+    else:
+        y = gemv_template(Wg, xg, cfg, row_q8(W) if cfg.weights == "int8" else None)
+    np.testing.assert_array_equal(y.cpu().numpy(), emulate(cfg, W, x))
+    height = cfg.tree_height(n)
+    checker = GpuBlockedChecker(Wg, 64, height, checks=8, generator=torch.Generator().manual_seed(4))
+    gpu = checker.verdict(xg, y).cpu().numpy()
+    cpu = BlockedChecker(W, x, 64, height).verdict_with_signs(
+        y.cpu().numpy(), checker.r.cpu().numpy().astype(np.float64)
+    )[0].all(0)
+    np.testing.assert_array_equal(gpu, cpu)
+    if is_exploit(cfg):
+        assert not gpu.all()
+    else:
+        assert gpu.all()
