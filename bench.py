@@ -9,7 +9,9 @@ exceeds L2 + MALL, so every step streams its weights from HBM, as decoding throu
 
 A 32-layer decode pass (the depth of Llama-3-8B) cycling over the layer copies is captured once
 in a HIP graph and replayed, as a decode loop replays its captured model (eager Python launches
-leave the GPU idle between kernels; their per-step time is reported beside).  Every GEMV output
+leave the GPU idle between kernels; their per-step time is reported beside).  The passes of the
+four modes below are replayed in alternating rounds, steps / 32 rounds of one pass each, and
+each figure is the median round.  Every GEMV output
 is checked by the trusted blocked checker in a later launch of the same stream: the checker's
 workgroups ride in a later GEMV launch (pck_gemv_group_check; bit-identical to a standalone
 check), the long gate/up and down launches, so their latency hides behind the weight stream.  The same pass with one standalone
@@ -135,6 +137,7 @@ def run_step(layer, with_check: bool, events=None):  # type: ignore[no-untyped-d
 
 
 MODE_GEMV, MODE_SERIAL, MODE_OVERLAP, MODE_RIDE = "gemv", "serial", "overlapped", "carried"
+MODES = (MODE_GEMV, MODE_SERIAL, MODE_OVERLAP, MODE_RIDE)
 
 # In carried mode the long launches of layer L also check outputs finished by earlier launches:
 # gate_up carries the previous layer's down and this layer's q, k, v, o; down carries gate and
@@ -222,20 +225,27 @@ def capture(layers, mode: str, depth: int):  # type: ignore[no-untyped-def]
     return graph, keep
 
 
-def timed_graph(graph, depth: int, reps: int) -> float:  # type: ignore[no-untyped-def]
-    """ms per layer of a captured pass replayed ``reps`` times."""
+def timed_modes(graphs: dict, depth: int, rounds: int) -> dict:  # type: ignore[type-arg]
+    """ms per layer of each captured pass: one warm replay each, then ``rounds`` rounds that
+    replay every pass once in turn; the median round per pass.  Alternating the passes gives
+    each the same clocks and cache state, which one back-to-back interval per pass, taken right
+    after its capture, did not."""
     import torch
 
-    graph.replay()
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(reps):
+    for graph in graphs.values():
         graph.replay()
-    end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / (reps * depth)
+    times: dict = {mode: [] for mode in graphs}  # type: ignore[type-arg]
+    for _ in range(rounds):
+        for mode, graph in graphs.items():
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record()
+            graph.replay()
+            end.record()
+            end.synchronize()
+            times[mode].append(start.elapsed_time(end) / depth)
+    return {mode: statistics.median(t) for mode, t in times.items()}
 
 
 def dominant_launch_ms(layers, reps: int) -> tuple[float, int]:  # type: ignore[no-untyped-def]
@@ -809,15 +819,13 @@ def main() -> None:
     depth = 32  # a Llama-3-8B decode pass
     reps = max(1, args.steps // depth)
     print("[bench] timing BF16 passes (HIP graphs)", file=sys.stderr, flush=True)
-    ms = {}
-    for mode in (MODE_GEMV, MODE_SERIAL, MODE_OVERLAP, MODE_RIDE):
-        graph, keep = capture(bf16_layers, mode, depth)
-        ms[mode] = timed_graph(graph, depth, reps)
-        if mode in (MODE_OVERLAP, MODE_RIDE):
-            verdicts = [r for item in keep if isinstance(item, list) for r in item]
-            assert len(verdicts) == 7 * depth, len(verdicts)
-            assert all(bool(r.verdict.all()) for r in verdicts), "checker rejected an honest output"
-        del graph, keep
+    captured = {mode: capture(bf16_layers, mode, depth) for mode in MODES}
+    ms = timed_modes({mode: graph for mode, (graph, _) in captured.items()}, depth, reps)
+    for mode in (MODE_OVERLAP, MODE_RIDE):
+        verdicts = [r for item in captured[mode][1] if isinstance(item, list) for r in item]
+        assert len(verdicts) == 7 * depth, len(verdicts)
+        assert all(bool(r.verdict.all()) for r in verdicts), "checker rejected an honest output"
+    del captured
     ms_eager, per_launch = (float("nan"), {}) if args.quick else timed(
         bf16_layers, args.steps, args.warmup, True, per_kernel=True
     )
@@ -830,14 +838,13 @@ def main() -> None:
     _, results = run_step(fp8_layers[0], True)
     assert all(bool(r.verdict.all()) for r in results), "checker rejected an honest FP8 output"
     bytes_fp8 = sum(gemv_bytes(m, n, 1) for _, m, n in LAYER)
-    ms8 = {}
-    for mode in (MODE_GEMV, MODE_SERIAL, MODE_OVERLAP, MODE_RIDE):
-        graph, keep = capture(fp8_layers, mode, depth)
-        ms8[mode] = timed_graph(graph, depth, reps)
-        if mode == MODE_RIDE:
-            verdicts = [r for item in keep if isinstance(item, list) for r in item]
-            assert all(bool(r.verdict.all()) for r in verdicts), "checker rejected an honest output"
-        del graph, keep
+    captured = {mode: capture(fp8_layers, mode, depth) for mode in MODES}
+    ms8 = timed_modes({mode: graph for mode, (graph, _) in captured.items()}, depth, reps)
+    for mode in (MODE_OVERLAP, MODE_RIDE):
+        verdicts = [r for item in captured[mode][1] if isinstance(item, list) for r in item]
+        assert len(verdicts) == 7 * depth, len(verdicts)
+        assert all(bool(r.verdict.all()) for r in verdicts), "checker rejected an honest output"
+    del captured
     del fp8_layers
     torch.cuda.empty_cache()
     ms_checked, ms_gemv_only = ms[MODE_RIDE], ms[MODE_GEMV]
