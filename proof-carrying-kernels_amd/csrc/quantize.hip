@@ -65,7 +65,7 @@ int pck_quantize_rows_q8(const void* W, int w_kind, int8_t* Wq, float* S, int64_
   if (W == nullptr || Wq == nullptr || S == nullptr) return hipErrorInvalidValue;
   const int64_t groups = (n + kQ8Group - 1) / kQ8Group;
   const int64_t blocks = (m * groups + 3) / 4;
-  if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;
+  if (blocks * 256 > 0xFFFFFFFFll) return hipErrorInvalidValue;  // 32-bit dispatch size
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (w_kind == 1) {
     quantize_rows_kernel<true><<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s>>>(

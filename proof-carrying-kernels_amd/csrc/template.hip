@@ -299,6 +299,7 @@ hipError_t launch_row(bool q8, const void* W, const float* S, const void* x, flo
   a.vector = n % vec == 0 && reinterpret_cast<uintptr_t>(W) % (elem * vec) == 0 &&
              reinterpret_cast<uintptr_t>(x) % (2 * vec) == 0;
   const int64_t blocks = (m + rows_per_block - 1) / rows_per_block;
+  if (blocks * threads > 0xFFFFFFFFll) return hipErrorInvalidValue;  // 32-bit dispatch size
   kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(threads), 0, stream>>>(a);
   return hipGetLastError();
 }
@@ -460,7 +461,8 @@ int pck_gemv_column(const void* WT, const void* x, float* y, float* scratch, uns
   const int64_t tiles = pck_column_tiles(m, vec);
   const int64_t rows_per_merge = splits > 1 ? kMergeThreads / (splits / 2) : 1;
   const int64_t merge_groups = (m + rows_per_merge - 1) / rows_per_merge;
-  if (tiles > 0x7FFFFFFF || merge_groups > 0x7FFFFFFF) return hipErrorInvalidValue;
+  if (tiles * threads > 0xFFFFFFFFll || merge_groups * kMergeThreads > 0xFFFFFFFFll)
+    return hipErrorInvalidValue;  // 32-bit dispatch size
   const ColumnArgs a{static_cast<const uint16_t*>(WT), static_cast<const uint16_t*>(x), y, scratch,
                      m, n, (n + splits - 1) / splits, skip_below};
   const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits));
