@@ -347,7 +347,21 @@ __global__ void __launch_bounds__(kWarp* kColMaxWarps) column_template_kernel(co
   float acc[VEC];
 #pragma unroll
   for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
-  for (int64_t j0 = j_begin + k; j0 < j_end; j0 += static_cast<int64_t>(kColAhead) * warps) {
+  const int64_t step = static_cast<int64_t>(kColAhead) * warps;
+  // With skipping, whether a column's weights are loaded depends on its activation, so the
+  // activations are loaded one iteration ahead: the weight loads then wait on nothing.
+  float x_ahead[kColAhead];
+  if constexpr (kSkip) {
+    const int64_t j_first = j_begin + k;
+    if (j_first < j_end) {
+#pragma unroll
+      for (int u = 0; u < kColAhead; ++u) {
+        const int64_t j = j_first + static_cast<int64_t>(u) * warps;
+        x_ahead[u] = bf16_bits(a.x[j < j_end ? j : j_first]);
+      }
+    }
+  }
+  for (int64_t j0 = j_begin + k; j0 < j_end; j0 += step) {
     uint32_t w[kColAhead][VEC / 2];
     float xs[kColAhead];
     bool use[kColAhead];
@@ -356,14 +370,22 @@ __global__ void __launch_bounds__(kWarp* kColMaxWarps) column_template_kernel(co
       const int64_t j = j0 + static_cast<int64_t>(u) * warps;
       const bool in = j < j_end;
       const int64_t at = in ? j : j0;
-      xs[u] = bf16_bits(a.x[at]);
       if constexpr (kSkip) {
         // The skipped column is never read: the exploit moves fewer bytes.
+        xs[u] = x_ahead[u];
         use[u] = in && active && !(fabsf(xs[u]) < a.skip_below);
         if (use[u]) load_row_vec<VEC>(a.WT + at * a.m + rr, w[u]);
       } else {
+        xs[u] = bf16_bits(a.x[at]);
         use[u] = in && active;
         load_row_vec<VEC>(a.WT + at * a.m + rr, w[u]);
+      }
+    }
+    if constexpr (kSkip) {
+#pragma unroll
+      for (int u = 0; u < kColAhead; ++u) {
+        const int64_t j = j0 + step + static_cast<int64_t>(u) * warps;
+        x_ahead[u] = bf16_bits(a.x[j < j_end ? j : j0]);
       }
     }
 #pragma unroll
