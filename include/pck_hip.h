@@ -160,6 +160,63 @@ typedef struct PckCheckBatch {
 int pck_blocked_check(const PckCheckBatch* batch, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
+ * In-pass checksums: the blocked check without a bank.  A GEMV launch that also writes, for
+ * every output row i, the FP64 pair (d_i, s_i) from the weights it streams anyway:
+ *   d_i = sum_j W_ij x_j      each product exact (one FMA per term, round to nearest)
+ *   s_i = sum_j |W_ij x_j|    the same with absolute values
+ * Lane l of the row's min(threads, 64) lanes adds its columns in the tree's own order
+ * (vector positions, then chains l, l + 64, ..., then the columns of a vector), starting
+ * from +0; the lanes then combine by an xor butterfly (offsets 32 .. 1, or 16 .. 1 at
+ * threads = 32).  The rows' y keep the bits of pck_gemv_group.
+ * A row-sum check then needs only (d, s), y and the signs of each block:
+ *   rho = sum_i r_i d_i - sum_i r_i y_i                       FP64, round to nearest
+ *   s   = s_factor * sum_i s_i, rounded up, then up to FP32    (s_factor bounds the RN sums)
+ *   tau = coef s + geps ((1 + u32) s + sum |y_i|) + tau_floor  every operation rounded up
+ * and the block passes only if its y are finite, tau is finite and |rho| <= tau: the blocked
+ * checker's relation (reference src/pck/cuda/csrc/checker_kernel.cu:115-183) with c . x
+ * replaced by r^T (W x) evaluated from exact products and s = a . |x| by its exact value
+ * (never above the bank's BF16 bound), so the threshold stays sound and is never looser.
+ * One wave per (check, block) pair: lane l takes rows l, l + 64, ... in order, then an xor
+ * butterfly (cx and r.y round to nearest, s and sum |y| round up).  No reference
+ * counterpart: the reference always reads a precomputed bank (src/pck/cuda/checker.py:91-104),
+ * 2.3% (BF16) / 4.7% (FP8) of the layer's bytes at b = 128.
+ * -------------------------------------------------------------------------------------------*/
+typedef struct PckRowSumCheckDesc {
+  const double* sums; /* (nb * b, 2) FP64 (d_i, s_i), 16-byte aligned                    */
+  const float* y;     /* (nb * b,) FP32 output under check                               */
+  const int8_t* r;    /* (K, nb, b) secret signs in {-1, +1}                             */
+  uint8_t* passed;    /* (K, nb) outputs: bool, rho, tau                                 */
+  double* rho;
+  double* tau;
+  int32_t block;
+  int32_t num_blocks;
+  int32_t checks;
+  int32_t reserved;   /* 0 */
+  double coef;        /* >= gamma_h + u32, rounded up                                    */
+  double geps;        /* >= gamma_H(u64), H >= D + ceil(b / 64) + 7                      */
+  double tau_floor;   /* >= n 2^-148                                                     */
+  double s_factor;    /* >= 1 / (1 - D 2^-53), D >= the row sums' depth: the max over    */
+                      /* threads T and vector width V of                                  */
+                      /* (T / min(T, 64)) ceil(ceil(n / V) / T) V + log2 min(T, 64)       */
+} PckRowSumCheckDesc;
+
+typedef struct PckRowSumBatch {
+  PckRowSumCheckDesc desc[PCK_MAX_BATCH];
+  int64_t start[PCK_MAX_BATCH + 1]; /* work item i belongs to check g if start[g] <= i < start[g+1] */
+  int32_t count;                    /* 0 .. PCK_MAX_BATCH (0: no checks) */
+} PckRowSumBatch;
+
+/* pck_gemv_group plus the row sums: sums[g] is GEMV g's (m, 2) FP64 output, 16-byte aligned.
+ * `ride` (NULL: none) holds row-sum checks of outputs that launches earlier on `stream`
+ * produced; their waves run in the first workgroups of the grid (one wave per (check, block)
+ * pair), and their results are bit-identical to pck_rowsum_check(ride). */
+int pck_gemv_group_rowsums(int weight_kind, const PckGemv* gemvs, double* const* sums, int count,
+                           int threads, const PckRowSumBatch* ride, void* stream);
+
+/* The row-sum checks of `batch` as one launch (four pairs per 256-lane workgroup). */
+int pck_rowsum_check(const PckRowSumBatch* batch, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
  * Blocked checker for a batch of activation rows (Y = X W^T, B >= 1): every column of Y is
  * checked as pck_blocked_check checks one GEMV output, against the same bank, signs and
  * constants (rho = c . X[b] - r . Y[b, beta rows] in FP64; tau as for pck_blocked_check with

@@ -11,6 +11,9 @@
 // (src/pck/cuda/csrc/checker.h:13-44); this kernel reads and writes neither, and counters stay
 // zero.  The same pairs can instead ride inside a later GEMV launch (pck_gemv_group_check),
 // with bit-identical results.
+//
+// Also here: the standalone launch of the row-sum check (rowsum_check.h), which needs no bank:
+// four (check, block) pairs per 256-lane workgroup, one wave each.
 
 #include <hip/hip_runtime.h>
 
@@ -18,6 +21,7 @@
 
 #include "check_pair.h"
 #include "pck_hip.h"
+#include "rowsum_check.h"
 
 namespace pck {
 namespace {
@@ -25,6 +29,15 @@ namespace {
 __global__ void __launch_bounds__(check::kThreads) blocked_check_kernel(const PckCheckBatch batch) {
   __shared__ check::Quad lds[check::kWaves];
   check::check_pair<8>(batch, blockIdx.x, lds);
+}
+
+constexpr int kRowSumWaves = 4;
+
+__global__ void __launch_bounds__(kRowSumWaves * rowsum::kWave)
+    rowsum_check_kernel(const PckRowSumBatch batch) {
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * kRowSumWaves +
+                       (static_cast<int>(threadIdx.x) >> 6);
+  if (item < rowsum::items(batch)) rowsum::check_item(batch, item);  // uniform per wave
 }
 
 }  // namespace
@@ -37,5 +50,17 @@ extern "C" int pck_blocked_check(const PckCheckBatch* batch, void* stream) {
     return hipErrorInvalidValue;  // the dispatch size is 32-bit in work-items
   pck::blocked_check_kernel<<<dim3(static_cast<unsigned>(items)), dim3(pck::check::kThreads), 0,
                               static_cast<hipStream_t>(stream)>>>(*batch);
+  return hipGetLastError();
+}
+
+extern "C" int pck_rowsum_check(const PckRowSumBatch* batch, void* stream) {
+  if (batch == nullptr || pck::rowsum::validate(*batch) != hipSuccess) return hipErrorInvalidValue;
+  const int64_t groups = (pck::rowsum::items(*batch) + pck::kRowSumWaves - 1) / pck::kRowSumWaves;
+  if (groups == 0) return hipSuccess;
+  if (groups * pck::kRowSumWaves * pck::rowsum::kWave > 0xFFFFFFFFll)
+    return hipErrorInvalidValue;  // the dispatch size is 32-bit in work-items
+  pck::rowsum_check_kernel<<<dim3(static_cast<unsigned>(groups)),
+                             dim3(pck::kRowSumWaves * pck::rowsum::kWave), 0,
+                             static_cast<hipStream_t>(stream)>>>(*batch);
   return hipGetLastError();
 }

@@ -32,6 +32,7 @@
 
 #include "check_pair.h"
 #include "pck_hip.h"
+#include "rowsum_check.h"
 
 namespace pck {
 namespace {
@@ -45,6 +46,7 @@ struct GemvItem {
   const void* W;
   const uint16_t* x;
   float* y;
+  double* sums;  // (m, 2) FP64 row sums (d_i, s_i) of the in-pass path; unused otherwise
   int64_t m;
   int64_t n;
   int64_t per_lane;  // vectors per virtual lane: ceil(ceil(n / vec) / T)
@@ -68,19 +70,40 @@ __device__ __forceinline__ float2 fp8_pair(uint32_t w) {
 
 __device__ __forceinline__ float fp8_one(uint8_t code) { return fp8_pair<false>(code).x; }
 
-// Adds the products of one vector to `acc`, in column order.
-template <bool kFp8>
-__device__ __forceinline__ void add_products(float& acc, const uint4& w, const uint4& xa,
-                                             const uint4& xb) {
+// Row sums of the in-pass path: d += w x and s += |w| |x| in FP64, each product exact (8 + 8 or
+// 4 + 8 significand bits, never underflowing in FP64), one rounding per term (the FMA's).
+struct RowSums {
+  double d = 0.0;
+  double s = 0.0;
+};
+
+template <bool kSums>
+__device__ __forceinline__ void add_sums(RowSums& rs, float w, float x) {
+  if constexpr (kSums) {
+    const double wd = static_cast<double>(w);
+    const double xd = static_cast<double>(x);
+    rs.d = __builtin_fma(wd, xd, rs.d);
+    rs.s = __builtin_fma(__builtin_fabs(wd), __builtin_fabs(xd), rs.s);
+  }
+}
+
+// Adds the products of one vector to `acc` (and, with kSums, to the row sums), in column order.
+template <bool kFp8, bool kSums = false>
+__device__ __forceinline__ void add_products(float& acc, RowSums& rs, const uint4& w,
+                                             const uint4& xa, const uint4& xb) {
   const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
   if constexpr (!kFp8) {
     const uint32_t xd[4] = {xa.x, xa.y, xa.z, xa.w};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const float p0 = bf16_lo(wd[k]) * bf16_lo(xd[k]);
-      const float p1 = bf16_hi(wd[k]) * bf16_hi(xd[k]);
+      const float w0 = bf16_lo(wd[k]), x0 = bf16_lo(xd[k]);
+      const float w1 = bf16_hi(wd[k]), x1 = bf16_hi(xd[k]);
+      const float p0 = w0 * x0;
+      const float p1 = w1 * x1;
       acc = acc + p0;
       acc = acc + p1;
+      add_sums<kSums>(rs, w0, x0);
+      add_sums<kSums>(rs, w1, x1);
     }
   } else {
     const uint32_t xd[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
@@ -88,31 +111,37 @@ __device__ __forceinline__ void add_products(float& acc, const uint4& w, const u
     for (int k = 0; k < 4; ++k) {
       const float2 f01 = fp8_pair<false>(wd[k]);
       const float2 f23 = fp8_pair<true>(wd[k]);
-      const float p0 = f01.x * bf16_lo(xd[2 * k]);
-      const float p1 = f01.y * bf16_hi(xd[2 * k]);
-      const float p2 = f23.x * bf16_lo(xd[2 * k + 1]);
-      const float p3 = f23.y * bf16_hi(xd[2 * k + 1]);
+      const float x0 = bf16_lo(xd[2 * k]), x1 = bf16_hi(xd[2 * k]);
+      const float x2 = bf16_lo(xd[2 * k + 1]), x3 = bf16_hi(xd[2 * k + 1]);
+      const float p0 = f01.x * x0;
+      const float p1 = f01.y * x1;
+      const float p2 = f23.x * x2;
+      const float p3 = f23.y * x3;
       acc = acc + p0;
       acc = acc + p1;
       acc = acc + p2;
       acc = acc + p3;
+      add_sums<kSums>(rs, f01.x, x0);
+      add_sums<kSums>(rs, f01.y, x1);
+      add_sums<kSums>(rs, f23.x, x2);
+      add_sums<kSums>(rs, f23.y, x3);
     }
   }
 }
 
 // Element loads for rows that cannot take 16-byte vectors (n not a multiple of the vector width
 // or a misaligned pointer): the same products in the same order, +0 past n.
-template <bool kFp8>
-__device__ __forceinline__ void add_products_scalar(float& acc, const void* w_row,
+template <bool kFp8, bool kSums = false>
+__device__ __forceinline__ void add_products_scalar(float& acc, RowSums& rs, const void* w_row,
                                                     const uint16_t* x, int64_t col, int64_t n) {
   constexpr int V = kFp8 ? 16 : 8;
 #pragma unroll
   for (int k = 0; k < V; ++k) {
     const int64_t j = col + k;
     float p = 0.0f;
+    float wv = 0.0f, xv = 0.0f;
     if (j < n) {
-      const float xv = __uint_as_float(static_cast<uint32_t>(x[j]) << 16);
-      float wv;
+      xv = __uint_as_float(static_cast<uint32_t>(x[j]) << 16);
       if constexpr (kFp8) {
         wv = fp8_one(static_cast<const uint8_t*>(w_row)[j]);
       } else {
@@ -121,6 +150,7 @@ __device__ __forceinline__ void add_products_scalar(float& acc, const void* w_ro
       p = wv * xv;
     }
     acc = acc + p;
+    add_sums<kSums>(rs, wv, xv);
   }
 }
 
@@ -166,7 +196,7 @@ __device__ __forceinline__ uint4 load_w(const unsigned char* p) {
   }
 }
 
-template <int T, int R, int U, bool kFp8, bool kVector, bool kPad, bool kNt>
+template <int T, int R, int U, bool kFp8, bool kVector, bool kPad, bool kNt, bool kSums = false>
 __device__ __forceinline__ void gemv_rows(const GemvBatch& batch, int64_t group) {
   constexpr int V = kFp8 ? 16 : 8;
   constexpr int kLanesPerRow = T >= kWave ? kWave : T;
@@ -202,6 +232,7 @@ __device__ __forceinline__ void gemv_rows(const GemvBatch& batch, int64_t group)
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int j = 0; j < kChains; ++j) acc[r][j] = -0.0f;
+  RowSums rs[R];  // per row: one FP64 pair per lane over all of its chains (kSums only)
 
   for (int64_t v0 = 0; v0 < P; v0 += U) {
     if constexpr (kVector) {
@@ -237,7 +268,8 @@ __device__ __forceinline__ void gemv_rows(const GemvBatch& batch, int64_t group)
         for (int r = 0; r < R; ++r)
 #pragma unroll
           for (int j = 0; j < kChains; ++j)
-            add_products<kFp8>(acc[r][j], wb[u][r][j], xa[u][j], kFp8 ? xb[u][j] : xa[u][j]);
+            add_products<kFp8, kSums>(acc[r][j], rs[r], wb[u][r][j], xa[u][j],
+                                      kFp8 ? xb[u][j] : xa[u][j]);
       }
     } else {
 #pragma unroll
@@ -245,9 +277,27 @@ __device__ __forceinline__ void gemv_rows(const GemvBatch& batch, int64_t group)
 #pragma unroll
         for (int j = 0; j < kChains; ++j) {
           const int64_t col = (v0 * T + chain0 + kLanesPerRow * j) * V;
-          add_products_scalar<kFp8>(acc[r][j], w_rows[r], x, col, n);
+          add_products_scalar<kFp8, kSums>(acc[r][j], rs[r], w_rows[r], x, col, n);
         }
       }
+    }
+  }
+
+  if constexpr (kSums) {
+    // The row's lanes combine their FP64 pairs by an xor butterfly (symmetric, so every lane of
+    // the row ends with the same pair); the row's first lane stores it as one 16-byte write.
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+      for (int off = kLanesPerRow / 2; off > 0; off /= 2) {
+        const double od = __shfl_xor(rs[r].d, off, kWave);
+        const double os = __shfl_xor(rs[r].s, off, kWave);
+        rs[r].d = rs[r].d + od;
+        rs[r].s = rs[r].s + os;
+      }
+      const int64_t row = (wave * kSlots + slot) * R + r;
+      if (chain0 == 0 && live[r])
+        reinterpret_cast<double2*>(it.sums)[row] = make_double2(rs[r].d, rs[r].s);
     }
   }
 
@@ -299,6 +349,24 @@ __global__ void __launch_bounds__(kGroupThreads)
     return;
   }
   gemv_rows<T, R, U, kFp8, true, kPad, kNt>(batch, static_cast<int64_t>(blockIdx.x) - items);
+}
+
+// The in-pass GEMV: the tree's outputs plus each row's FP64 sums (d_i, s_i), and in the first
+// workgroups of the grid the row-sum checks of `ride` (outputs of earlier launches on the stream,
+// read from memory; one wave per (check, block) pair, the code of pck_rowsum_check, so the
+// results are bit-identical to it).  A check never reads anything this launch writes.
+template <int T, int R, int U, bool kFp8, bool kVector, bool kPad, bool kNt>
+__global__ void __launch_bounds__(kGroupThreads)
+    gemv_rowsum_kernel(const GemvBatch batch, const PckRowSumBatch ride) {
+  const int64_t items = rowsum::items(ride);
+  const int64_t ride_groups = (items + kWavesPerGroup - 1) / kWavesPerGroup;
+  const int64_t group = static_cast<int64_t>(blockIdx.x);
+  if (group < ride_groups) {
+    const int64_t item = group * kWavesPerGroup + (static_cast<int>(threadIdx.x) >> 6);
+    if (item < items) rowsum::check_item(ride, item);  // uniform per wave
+    return;
+  }
+  gemv_rows<T, R, U, kFp8, kVector, kPad, kNt, true>(batch, group - ride_groups);
 }
 
 // Naive tree: one workgroup of `threads` lanes per row (reference gemv_kernel.cu:27-55).
@@ -361,51 +429,63 @@ int64_t plan_groups(GemvBatch& batch, int64_t rows_per_group) {
   return batch.first_group[batch.count];
 }
 
-template <int T, int R, int U, bool kFp8, bool kVector, bool kPad, bool kNt>
-hipError_t launch_tree(GemvBatch& batch, hipStream_t stream) {
+// kSums: the in-pass kernel, with `rs` the row-sum checks it carries; otherwise the plain tree.
+template <int T, int R, int U, bool kFp8, bool kVector, bool kPad, bool kNt, bool kSums>
+hipError_t launch_tree(GemvBatch& batch, const PckRowSumBatch* rs, hipStream_t stream) {
   constexpr int kLanesPerRow = T >= kWave ? kWave : T;
   const int64_t groups = plan_groups(batch, (kWave / kLanesPerRow) * R * kWavesPerGroup);
-  if (groups == 0) return hipSuccess;
-  if (groups * kGroupThreads > 0xFFFFFFFFll) return hipErrorInvalidValue;  // 32-bit dispatch size
-  gemv_tree_kernel<T, R, U, kFp8, kVector, kPad, kNt>
-      <<<dim3(static_cast<unsigned>(groups)), dim3(kGroupThreads), 0, stream>>>(batch);
+  if constexpr (kSums) {
+    const int64_t total = groups + (rowsum::items(*rs) + kWavesPerGroup - 1) / kWavesPerGroup;
+    if (total == 0) return hipSuccess;
+    if (total * kGroupThreads > 0xFFFFFFFFll) return hipErrorInvalidValue;  // 32-bit dispatch
+    gemv_rowsum_kernel<T, R, U, kFp8, kVector, kPad, kNt>
+        <<<dim3(static_cast<unsigned>(total)), dim3(kGroupThreads), 0, stream>>>(batch, *rs);
+  } else {
+    (void)rs;
+    if (groups == 0) return hipSuccess;
+    if (groups * kGroupThreads > 0xFFFFFFFFll) return hipErrorInvalidValue;  // 32-bit dispatch
+    gemv_tree_kernel<T, R, U, kFp8, kVector, kPad, kNt>
+        <<<dim3(static_cast<unsigned>(groups)), dim3(kGroupThreads), 0, stream>>>(batch);
+  }
   return hipGetLastError();
 }
 
-template <int T, int R, bool kFp8, bool kPad, bool kNt>
-hipError_t launch_unroll(GemvBatch& batch, int unroll, hipStream_t s) {
-  if (unroll >= 4) return launch_tree<T, R, 4, kFp8, true, kPad, kNt>(batch, s);
-  if (unroll == 2) return launch_tree<T, R, 2, kFp8, true, kPad, kNt>(batch, s);
-  return launch_tree<T, R, 1, kFp8, true, kPad, kNt>(batch, s);
+template <int T, int R, bool kFp8, bool kPad, bool kNt, bool kSums>
+hipError_t launch_unroll(GemvBatch& batch, int unroll, const PckRowSumBatch* rs, hipStream_t s) {
+  if (unroll >= 4) return launch_tree<T, R, 4, kFp8, true, kPad, kNt, kSums>(batch, rs, s);
+  if (unroll == 2) return launch_tree<T, R, 2, kFp8, true, kPad, kNt, kSums>(batch, rs, s);
+  return launch_tree<T, R, 1, kFp8, true, kPad, kNt, kSums>(batch, rs, s);
 }
 
-template <int T, bool kFp8, bool kPad>
-hipError_t launch_vector(GemvBatch& batch, TreeShape shape, hipStream_t s) {
+template <int T, bool kFp8, bool kPad, bool kSums>
+hipError_t launch_vector(GemvBatch& batch, TreeShape shape, const PckRowSumBatch* rs,
+                         hipStream_t s) {
   if constexpr (T == 256) {
     const bool nt = shape.nt != 0;
+    const int u = shape.unroll;
     switch (shape.rows) {
       case 4:
-        return nt ? launch_unroll<T, 4, kFp8, kPad, true>(batch, shape.unroll, s)
-                  : launch_unroll<T, 4, kFp8, kPad, false>(batch, shape.unroll, s);
+        return nt ? launch_unroll<T, 4, kFp8, kPad, true, kSums>(batch, u, rs, s)
+                  : launch_unroll<T, 4, kFp8, kPad, false, kSums>(batch, u, rs, s);
       case 2:
-        return nt ? launch_unroll<T, 2, kFp8, kPad, true>(batch, shape.unroll, s)
-                  : launch_unroll<T, 2, kFp8, kPad, false>(batch, shape.unroll, s);
+        return nt ? launch_unroll<T, 2, kFp8, kPad, true, kSums>(batch, u, rs, s)
+                  : launch_unroll<T, 2, kFp8, kPad, false, kSums>(batch, u, rs, s);
       default:
-        return nt ? launch_unroll<T, 1, kFp8, kPad, true>(batch, shape.unroll, s)
-                  : launch_unroll<T, 1, kFp8, kPad, false>(batch, shape.unroll, s);
+        return nt ? launch_unroll<T, 1, kFp8, kPad, true, kSums>(batch, u, rs, s)
+                  : launch_unroll<T, 1, kFp8, kPad, false, kSums>(batch, u, rs, s);
     }
   } else {
     (void)shape;
-    return launch_tree<T, 1, 2, kFp8, true, kPad, false>(batch, s);
+    return launch_tree<T, 1, 2, kFp8, true, kPad, false, kSums>(batch, rs, s);
   }
 }
 
-template <int T, bool kFp8>
+template <int T, bool kFp8, bool kSums = false>
 hipError_t launch_for_threads(GemvBatch& batch, bool vector, bool pad, TreeShape shape,
-                              hipStream_t s) {
-  if (!vector) return launch_tree<T, 1, 1, kFp8, false, true, false>(batch, s);
-  return pad ? launch_vector<T, kFp8, true>(batch, shape, s)
-             : launch_vector<T, kFp8, false>(batch, shape, s);
+                              hipStream_t s, const PckRowSumBatch* rs = nullptr) {
+  if (!vector) return launch_tree<T, 1, 1, kFp8, false, true, false, kSums>(batch, rs, s);
+  return pad ? launch_vector<T, kFp8, true, kSums>(batch, shape, rs, s)
+             : launch_vector<T, kFp8, false, kSums>(batch, shape, rs, s);
 }
 
 template <int R, int U, bool kFp8, bool kPad, bool kNt = true>
@@ -440,32 +520,55 @@ hipError_t launch_ride(GemvBatch& batch, bool pad, int64_t per_lane, const PckCh
   }
 }
 
+// The launch plan of a group: validated items, whether every row takes 16-byte vectors, whether
+// any chain has padding vectors, the longest chain and the total rows.
+struct GroupPlan {
+  GemvBatch batch{};
+  bool vector = true;
+  bool pad = false;
+  int64_t max_per_lane = 1;
+  int64_t rows = 0;
+};
+
 template <bool kFp8>
-hipError_t launch_group(const PckGemv* gemvs, int count, int threads, const PckCheckBatch* ride,
-                        hipStream_t stream) {
+hipError_t plan_group(const PckGemv* gemvs, double* const* sums, int count, int threads,
+                      GroupPlan& plan) {
   constexpr int V = kFp8 ? 16 : 8;
   if (count < 1 || count > PCK_MAX_GROUP || gemvs == nullptr) return hipErrorInvalidValue;
   if (threads < kWarp || threads > 1024 || (threads & (threads - 1)) != 0)
     return hipErrorInvalidValue;
-  GemvBatch batch{};
-  batch.count = count;
-  bool vector = true;
-  bool pad = false;
-  int64_t max_per_lane = 1;
+  plan.batch.count = count;
   for (int g = 0; g < count; ++g) {
     const PckGemv& d = gemvs[g];
     if (d.m < 0 || d.m > 0x7FFFFFFF || (d.m > 0 && (d.n < 1 || !d.W || !d.x || !d.y)))
       return hipErrorInvalidValue;
+    double* rs = sums != nullptr ? sums[g] : nullptr;
+    if (sums != nullptr && d.m > 0 && (rs == nullptr || reinterpret_cast<uintptr_t>(rs) % 16 != 0))
+      return hipErrorInvalidValue;
     const int64_t n = d.m > 0 ? d.n : 1;
     const int64_t per_lane = ((n + V - 1) / V + threads - 1) / threads;
-    batch.item[g] = GemvItem{d.W, static_cast<const uint16_t*>(d.x), d.y, d.m, n, per_lane};
+    plan.batch.item[g] =
+        GemvItem{d.W, static_cast<const uint16_t*>(d.x), d.y, rs, d.m, n, per_lane};
+    plan.rows += d.m;
     if (d.m > 0) {
-      vector = vector && n % V == 0 && reinterpret_cast<uintptr_t>(d.W) % 16 == 0 &&
-               reinterpret_cast<uintptr_t>(d.x) % 16 == 0;
-      max_per_lane = per_lane > max_per_lane ? per_lane : max_per_lane;
-      pad = pad || n % (static_cast<int64_t>(threads) * V) != 0;
+      plan.vector = plan.vector && n % V == 0 && reinterpret_cast<uintptr_t>(d.W) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(d.x) % 16 == 0;
+      plan.max_per_lane = per_lane > plan.max_per_lane ? per_lane : plan.max_per_lane;
+      plan.pad = plan.pad || n % (static_cast<int64_t>(threads) * V) != 0;
     }
   }
+  return hipSuccess;
+}
+
+template <bool kFp8>
+hipError_t launch_group(const PckGemv* gemvs, int count, int threads, const PckCheckBatch* ride,
+                        hipStream_t stream) {
+  GroupPlan plan;
+  if (plan_group<kFp8>(gemvs, nullptr, count, threads, plan) != hipSuccess)
+    return hipErrorInvalidValue;
+  GemvBatch& batch = plan.batch;
+  const bool vector = plan.vector, pad = plan.pad;
+  const int64_t max_per_lane = plan.max_per_lane;
   if (ride != nullptr) {
     if (check::validate(*ride) != hipSuccess) return hipErrorInvalidValue;
     if (threads == 256 && vector) {
@@ -479,9 +582,7 @@ hipError_t launch_group(const PckGemv* gemvs, int count, int threads, const PckC
     const int err = pck_blocked_check(ride, stream);
     if (err != 0) return static_cast<hipError_t>(err);
   }
-  int64_t rows = 0;
-  for (int g = 0; g < count; ++g) rows += batch.item[g].m;
-  const TreeShape shape = choose_shape(max_per_lane, rows, kFp8);
+  const TreeShape shape = choose_shape(max_per_lane, plan.rows, kFp8);
   switch (threads) {
     case 32: return launch_for_threads<32, kFp8>(batch, vector, pad, shape, stream);
     case 64: return launch_for_threads<64, kFp8>(batch, vector, pad, shape, stream);
@@ -489,6 +590,34 @@ hipError_t launch_group(const PckGemv* gemvs, int count, int threads, const PckC
     case 256: return launch_for_threads<256, kFp8>(batch, vector, pad, shape, stream);
     case 512: return launch_for_threads<512, kFp8>(batch, vector, pad, shape, stream);
     default: return launch_for_threads<1024, kFp8>(batch, vector, pad, shape, stream);
+  }
+}
+
+// Launch shape of the in-pass kernel (pck_gemv_set_shape overrides it as for the plain tree).
+TreeShape choose_rowsum_shape(int64_t per_lane, int64_t rows, bool fp8) {
+  return choose_shape(per_lane, rows, fp8);
+}
+
+template <bool kFp8>
+hipError_t launch_group_rowsums(const PckGemv* gemvs, double* const* sums, int count, int threads,
+                                const PckRowSumBatch* ride, hipStream_t stream) {
+  if (sums == nullptr) return hipErrorInvalidValue;
+  GroupPlan plan;
+  if (plan_group<kFp8>(gemvs, sums, count, threads, plan) != hipSuccess)
+    return hipErrorInvalidValue;
+  PckRowSumBatch none{};
+  const PckRowSumBatch* rs = ride != nullptr ? ride : &none;
+  if (rowsum::validate(*rs) != hipSuccess) return hipErrorInvalidValue;
+  GemvBatch& b = plan.batch;
+  const TreeShape shape = choose_rowsum_shape(plan.max_per_lane, plan.rows, kFp8);
+  const bool v = plan.vector, p = plan.pad;
+  switch (threads) {
+    case 32: return launch_for_threads<32, kFp8, true>(b, v, p, shape, stream, rs);
+    case 64: return launch_for_threads<64, kFp8, true>(b, v, p, shape, stream, rs);
+    case 128: return launch_for_threads<128, kFp8, true>(b, v, p, shape, stream, rs);
+    case 256: return launch_for_threads<256, kFp8, true>(b, v, p, shape, stream, rs);
+    case 512: return launch_for_threads<512, kFp8, true>(b, v, p, shape, stream, rs);
+    default: return launch_for_threads<1024, kFp8, true>(b, v, p, shape, stream, rs);
   }
 }
 
@@ -514,6 +643,14 @@ int pck_gemv_group_check(int weight_kind, const PckGemv* gemvs, int count, int t
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (weight_kind == 0) return pck::launch_group<false>(gemvs, count, threads, ride, s);
   if (weight_kind == 1) return pck::launch_group<true>(gemvs, count, threads, ride, s);
+  return hipErrorInvalidValue;
+}
+
+int pck_gemv_group_rowsums(int weight_kind, const PckGemv* gemvs, double* const* sums, int count,
+                           int threads, const PckRowSumBatch* ride, void* stream) {
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (weight_kind == 0) return pck::launch_group_rowsums<false>(gemvs, sums, count, threads, ride, s);
+  if (weight_kind == 1) return pck::launch_group_rowsums<true>(gemvs, sums, count, threads, ride, s);
   return hipErrorInvalidValue;
 }
 

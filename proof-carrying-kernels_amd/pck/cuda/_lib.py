@@ -85,6 +85,33 @@ class PckBatchCheckDesc(ctypes.Structure):
     ]
 
 
+class PckRowSumCheckDesc(ctypes.Structure):
+    _fields_ = [
+        ("sums", _p),
+        ("y", _p),
+        ("r", _p),
+        ("passed", _p),
+        ("rho", _p),
+        ("tau", _p),
+        ("block", _i32),
+        ("num_blocks", _i32),
+        ("checks", _i32),
+        ("reserved", _i32),
+        ("coef", _f64),
+        ("geps", _f64),
+        ("tau_floor", _f64),
+        ("s_factor", _f64),
+    ]
+
+
+class PckRowSumBatch(ctypes.Structure):
+    _fields_ = [
+        ("desc", PckRowSumCheckDesc * MAX_BATCH),
+        ("start", _i64 * (MAX_BATCH + 1)),
+        ("count", _i32),
+    ]
+
+
 # name -> (argtypes); every entry point returns int (a hipError_t value)
 SIGNATURES: dict[str, list[Any]] = {
     "pck_gemv_bf16_naive": [_p, _p, _p, _i64, _i64, _int, _p],
@@ -98,6 +125,10 @@ SIGNATURES: dict[str, list[Any]] = {
     "pck_bgemm_pack": [_int, _p, _p, _i64, _i64, _p],
     "pck_bgemm_packed": [_int, _p, _p, _p, _i64, _i64, _i64, _p],
     "pck_blocked_check": [ctypes.POINTER(PckCheckBatch), _p],
+    "pck_gemv_group_rowsums": [
+        _int, ctypes.POINTER(PckGemv), ctypes.POINTER(_p), _int, _int, _p, _p,
+    ],  # fmt: skip
+    "pck_rowsum_check": [ctypes.POINTER(PckRowSumBatch), _p],
     "pck_batch_check_workspace": [ctypes.POINTER(PckBatchCheckDesc), _int, ctypes.POINTER(_i64)],
     "pck_batch_check": [ctypes.POINTER(PckBatchCheckDesc), _int, _p, _i64, _p],
     "pck_read_stream": [_p, _i64, _p, _int, _p],

@@ -13,6 +13,7 @@ import ctypes
 import math
 from collections.abc import Sequence
 from dataclasses import dataclass
+from typing import Any
 
 import torch
 
@@ -21,6 +22,8 @@ from pck.cuda._lib import (
     PckBatchCheckDesc,
     PckCheckBatch,
     PckCheckDesc,
+    PckRowSumBatch,
+    PckRowSumCheckDesc,
     check,
     lib,
     stream_handle,
@@ -337,6 +340,138 @@ def check_many(
             [ch.tau_floor for ch, _, _ in chunk],
         )
         results.extend(CheckResult(passed, rho, tau) for passed, rho, tau in outputs)
+    return results
+
+
+def rowsum_depth(n: int) -> int:
+    """Depth D of the in-pass row sums of a row of n columns, for every launch: the most
+    additions any term passes through, over thread counts 32..1024 and vectors of 8 or 16
+    columns.  Lane l of min(T, 64) lanes adds (T / min(T, 64)) ceil(ceil(n / V) / T) V terms in
+    sequence (padding included: adding +0 is exact), then log2 min(T, 64) butterfly levels."""
+    depth = 0
+    for threads in (32, 64, 128, 256, 512, 1024):
+        lanes = min(threads, 64)
+        for vec in (8, 16):
+            per_lane = (threads // lanes) * ceil_div(ceil_div(n, vec), threads) * vec
+            depth = max(depth, per_lane + lanes.bit_length() - 1)
+    return depth
+
+
+class RowSumChecker:
+    """Blocked checks of y = W x from the row sums of an in-pass GEMV launch, with no bank.
+
+    The in-pass launch (`pck.cuda.gemv_group_rowsums`) writes, beside y, the FP64 pair
+    (d_i, s_i) = (sum_j W_ij x_j, sum_j |W_ij x_j|) of every row from the weights it streams,
+    so the check reads 16 bytes per row instead of the bank's 6n bytes per block (2.3% of BF16
+    and 4.7% of FP8 weight bytes at b = 128).  Each (check, block) pair is then the blocked
+    checker's relation (reference `src/pck/cuda/csrc/checker_kernel.cu:115-183`):
+    rho = r . d_beta - r . y_beta and tau = coef s + geps ((1 + u32) s + sum |y|) + tau_floor,
+    with s the exact sum of |W_ij x_j| over the block bounded above.  That s never exceeds the
+    bank's a . |x|, so this threshold is never looser than `GpuBlockedChecker`'s, and it is
+    sound for the same reason (T2/T3: the honest tree error is within coef s; rho's own FP64
+    error within geps).  Signs come from the same draw as `GpuBlockedChecker` (the same
+    generator state gives the same r), ``coef`` and ``tau_floor`` are its values; ``s_factor``
+    = 1 + (D + 1) 2^-52 >= 1 / (1 - D u64) bounds the RN row sums of depth D = `rowsum_depth`
+    (n), and ``geps`` = gamma_H(u64) covers rho's FP64 evaluation, H = D + ceil(b / 64) + 7
+    (the row sums, the check's per-lane sums and butterfly, the final subtraction).  H is far
+    below the bank checker's n + b + 1, so this tau is never above `GpuBlockedChecker`'s.
+
+    The check runs inside the producing GEMV's launch sequence: it suits the production
+    (non-adversarial) fault model, as the bank checker with signs drawn at weight load does
+    (reference `src/pck/cuda/checker.py:4-6`); the bank checker stays the trusted reference.
+    """
+
+    def __init__(
+        self,
+        m: int,
+        n: int,
+        block: int,
+        height: int,
+        checks: int = 1,
+        generator: torch.Generator | None = None,
+        device: torch.device | str | None = None,
+    ) -> None:
+        if block < 1 or m % block:
+            raise ValueError(f"block={block} must be positive and divide m={m}")
+        if checks < 1:
+            raise ValueError(f"checks must be positive, got {checks}")
+        if n < 1:
+            raise ValueError(f"n must be positive, got {n}")
+        device = torch.device("cuda") if device is None else torch.device(device)
+        self.m, self.n, self.block, self.checks = m, n, block, checks
+        self.num_blocks = m // block
+        bits = torch.randint(0, 2, (checks, self.num_blocks, block), generator=generator)
+        self.r = (2 * bits - 1).to(torch.int8).to(device)
+        depth = rowsum_depth(n)
+        self.coef = next_up(gamma(height) + U32, 2)
+        self.geps = next_up(gamma(depth + ceil_div(block, 64) + 7, U64), 2)
+        self.tau_floor = next_up(n * 2.0**-148, 2)
+        self.s_factor = next_up(1.0 + (depth + 1) * 2.0**-52, 2)
+
+    @property
+    def device(self) -> torch.device:
+        return self.r.device
+
+    def check(self, sums: torch.Tensor, y: torch.Tensor) -> CheckResult:
+        """Run every check on output ``y`` with its row sums ``sums`` (m, 2) FP64."""
+        return rowsum_check_many([(self, sums, y)])[0]
+
+    def verdict(self, sums: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+        """Per-block pass/fail (True = passed every check)."""
+        return self.check(sums, y).verdict
+
+
+def rowsum_batch_for(
+    items: Sequence[tuple[RowSumChecker, torch.Tensor, torch.Tensor]],
+) -> tuple[Any, list[CheckResult], torch.device]:
+    """Validates up to eight ``(RowSumChecker, sums, y)`` items and returns the launch
+    descriptor (a `PckRowSumBatch`), freshly allocated results and the device."""
+    if not 1 <= len(items) <= MAX_BATCH:
+        raise RuntimeError(f"batch size must be in [1, {MAX_BATCH}], got {len(items)}")
+    device = items[0][0].device
+    batch = PckRowSumBatch()
+    batch.count = len(items)
+    results = []
+    for g, (ch, sums, y) in enumerate(items):
+        _check_tensor(sums, "sums", torch.float64, device)
+        _check_tensor(y, "y", torch.float32, device)
+        if ch.device != device:
+            raise RuntimeError(f"the checker's signs must be on {device}")
+        if tuple(sums.shape) != (ch.m, 2):
+            raise RuntimeError(f"sums must have shape ({ch.m}, 2), got {list(sums.shape)}")
+        if tuple(y.shape) != (ch.m,):
+            raise RuntimeError(f"y must have shape ({ch.m},), got {list(y.shape)}")
+        if sums.data_ptr() % 16:
+            raise RuntimeError("sums must be 16-byte aligned")
+        shape = (ch.checks, ch.num_blocks)
+        passed = torch.empty(shape, dtype=torch.bool, device=device)
+        rho = torch.empty(shape, dtype=torch.float64, device=device)
+        tau = torch.empty(shape, dtype=torch.float64, device=device)
+        batch.desc[g] = PckRowSumCheckDesc(
+            sums.data_ptr(), y.data_ptr(), ch.r.data_ptr(), passed.data_ptr(), rho.data_ptr(),
+            tau.data_ptr(), ch.block, ch.num_blocks, ch.checks, 0, ch.coef, ch.geps,
+            ch.tau_floor, ch.s_factor,
+        )  # fmt: skip
+        batch.start[g + 1] = batch.start[g] + ch.checks * ch.num_blocks
+        results.append(CheckResult(passed, rho, tau))
+    if batch.start[batch.count] > 2**31 - 1:
+        raise RuntimeError("too many blocks")
+    return batch, results, device
+
+
+def rowsum_check_many(
+    items: Sequence[tuple[RowSumChecker, torch.Tensor, torch.Tensor]],
+) -> list[CheckResult]:
+    """Row-sum checks of several outputs, ``(checker, sums, y)`` each, eight per launch
+    (`pck_rowsum_check`).  A row-sum check uses no scratch, so a checker may appear more than
+    once."""
+    results: list[CheckResult] = []
+    for i in range(0, len(items), MAX_BATCH):
+        batch, res, device = rowsum_batch_for(items[i : i + MAX_BATCH])
+        with torch.cuda.device(device):
+            err = lib().pck_rowsum_check(batch, stream_handle(device))
+        check(err, "row-sum check launch")
+        results.extend(res)
     return results
 
 

@@ -167,3 +167,54 @@ def gemv_group(
         err = lib().pck_gemv_group(kind, descs, len(pairs), threads, stream_handle(device))
     check(err, "grouped gemv launch")
     return outs
+
+
+def gemv_group_rowsums(
+    pairs: Sequence[tuple[torch.Tensor, torch.Tensor]],
+    checks: Sequence[tuple[Any, torch.Tensor, torch.Tensor]] = (),
+    threads: int = 256,
+) -> tuple[list[torch.Tensor], list[torch.Tensor], list[Any]]:
+    """In-pass GEMVs: `gemv_group` plus, for every GEMV, its row sums (m, 2) FP64
+    (d_i = sum_j W_ij x_j and s_i = sum_j |W_ij x_j|, exact products, rounded-to-nearest sums in
+    a fixed order) from the weights the launch streams anyway, and, in the same launch, the
+    row-sum checks of ``checks``: up to eight ``(RowSumChecker, sums, y)`` items whose outputs
+    came from earlier launches on this stream.  Returns (outputs, sums, check results); the
+    outputs have exactly the bits of `gemv_group`, the results those of
+    ``rowsum_check_many(checks)``.  No reference counterpart: the reference checks against a
+    bank built at weight load (`src/pck/cuda/checker.py:91-104`)."""
+    from pck.cuda.checker import rowsum_batch_for
+
+    descs, outs, kind, device = _group_descriptors(pairs, threads)
+    sums = [torch.empty((W.size(0), 2), dtype=torch.float64, device=device) for W, _ in pairs]
+    ptrs = (ctypes.c_void_p * len(sums))(*[s.data_ptr() for s in sums])
+    ride = None
+    results: list[Any] = []
+    if checks:
+        ride, results, check_device = rowsum_batch_for(checks)
+        if check_device != device:
+            raise RuntimeError("the checks must be on the GEMVs' device")
+    with torch.cuda.device(device):
+        err = lib().pck_gemv_group_rowsums(
+            kind, descs, ptrs, len(pairs), threads, None if ride is None else ctypes.byref(ride),
+            stream_handle(device),
+        )  # fmt: skip
+    check(err, "in-pass gemv launch")
+    return outs, sums, results
+
+
+def gemv_coalesced_rowsums(
+    W: torch.Tensor, x: torch.Tensor, threads: int = 256
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """(y, sums): `gemv_coalesced` and the row sums of the in-pass launch."""
+    _validate(W, x, threads, 32, torch.bfloat16)
+    outs, sums, _ = gemv_group_rowsums([(W, x)], (), threads)
+    return outs[0], sums[0]
+
+
+def gemv_fp8_rowsums(
+    Q: torch.Tensor, x: torch.Tensor, threads: int = 256
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """(z, sums): `gemv_fp8` and the row sums of the in-pass launch (of Q itself, unscaled)."""
+    _validate(Q, x, threads, 32, torch.float8_e4m3fn)
+    outs, sums, _ = gemv_group_rowsums([(Q, x)], (), threads)
+    return outs[0], sums[0]
