@@ -43,7 +43,6 @@ namespace pck {
 namespace {
 
 constexpr int kWarp = 32;
-constexpr int kWave = 64;
 constexpr int kMaxThreads = 1024;
 constexpr int kQ8Group = 128;
 

@@ -8,7 +8,13 @@ Flags that the numerics depend on:
   -ffp-contract=off   no mul + add -> FMA contraction (the GEMV adds rounded products, and the
                       checker's error-free transformations need separate roundings);
   no -ffast-math and no denormal flushing (kernel descriptors keep FP32/FP64 denormals);
-  -target-feature -packed-fp32-ops   no packed FP32 instructions in any kernel.
+  -Xclang -target-feature -Xclang -packed-fp32-ops
+                      no packed FP32 instructions (v_pk_add/mul/fma_f32) in any kernel.  The
+                      gfx950 device pass applies it (without it hipcc -O3 forms v_pk_fma_f32
+                      from ordinary float2 code; tests/test_build_flags.py shows both); the x86
+                      host pass prints "'-packed-fp32-ops' is not a recognized feature for this
+                      target (ignoring feature)", which concerns host code only;
+  -Wall -Wextra -Werror   every warning of the device and host passes fails the build.
 """
 
 from __future__ import annotations
@@ -46,6 +52,8 @@ HIPCC_FLAGS = [
     "-ffp-contract=off",
     "-fno-fast-math",
     "-Wall",
+    "-Wextra",
+    "-Werror",
     "-Xclang",
     "-target-feature",
     "-Xclang",

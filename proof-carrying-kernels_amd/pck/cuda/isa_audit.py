@@ -167,7 +167,8 @@ def compile_to_asm(source: str, out_dir: Path) -> str:
     cmd = [
         _build.hipcc(), *_build.HIPCC_FLAGS, *_build.SOURCE_FLAGS.get(source, []),
         f"-I{_build.INCLUDE}", f"-I{_build.CSRC}", "--cuda-device-only", "-S",
-        str(_build.CSRC / source), "-o", str(out),
+        # hipcc adds --hip-link, which a compile to assembly does not use
+        "-Wno-unused-command-line-argument", str(_build.CSRC / source), "-o", str(out),
     ]  # fmt: skip
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:

@@ -1,33 +1,41 @@
-"""Pinned checker hash and per-variant manifests (reference `src/pck/manifest.py`).
+"""The pinned trusted checker and per-variant certificates (interface of the reference's
+`src/pck/manifest.py`: `verify_pinned`, `CheckerMismatch`, `Manifest`, ``--update``).
 
-The trusted checker's files are hash-pinned in ``checker_lock.json``: `verify_pinned` raises
-if the code on disk does not match, and a test keeps the lock current.  On MI355X the trusted
-set is this build's: the host checkers and constants, the HIP kernels of the checkers and of
-the products whose trees they bound, the rounding helpers, the C ABI header, the ctypes
-signatures and the build script (its compiler flags are part of what the bounds assume:
-no contraction, no fast math, no packed FP32).  A `Manifest` records what a certified variant
-rests on: its config, the spec's parameters, the checker hash, the Lean hash when the Lean
-sources are present (they are not in this build), the theorem names and the commit.
+What is pinned.  The verdicts of this build rest on three things, and the lock
+(``checker_lock.json``) records all three:
 
-Update the lock after a deliberate change to a trusted file:
-  python -m pck.manifest --update
+- the trusted source files: the host-side constants and wrappers, the HIP kernels of the
+  checkers and of the products whose trees the thresholds bound, the rounding helpers, the C
+  ABI header and the ctypes signatures (`TRUSTED`), each by its SHA-256;
+- the compiler flags and target the library is built with (`pck._build`): no contraction, no
+  fast math, no packed FP32, gfx950.  They are recorded as data, so a change of flags is
+  reported as such, not as an anonymous change of the build script;
+- a digest over both, which is what a certificate quotes (`checker_hash`).
+
+`verify_pinned` raises `CheckerMismatch` naming every file or setting that differs from the
+lock.  After a reviewed change: ``python -m pck.manifest --update``.
+
+A `Manifest` is the certificate of one variant: its task, config, slot code, the spec's
+parameters, the speedup, the checker digest, the digest of Lean sources when a ``lean/``
+directory is present (this build has none), the theorems it rests on and the commit.
 """
 
 from __future__ import annotations
 
 import argparse
-import functools
 import hashlib
 import json
-import subprocess
 from dataclasses import asdict, dataclass, field
 from pathlib import Path
 from typing import Any
 
-SRC = Path(__file__).parent  # proof-carrying-kernels_amd/pck
-PACKAGE_ROOT = SRC.parent  # proof-carrying-kernels_amd
+PACKAGE = Path(__file__).resolve().parent  # proof-carrying-kernels_amd/pck
+PACKAGE_ROOT = PACKAGE.parent  # proof-carrying-kernels_amd
 ROOT = PACKAGE_ROOT.parent  # the repository
-LOCK = SRC / "checker_lock.json"
+LOCK = PACKAGE / "checker_lock.json"
+LOCK_FORMAT = 2
+
+# Paths relative to PACKAGE_ROOT.
 TRUSTED = (
     "pck/fp.py",
     "pck/member.py",
@@ -37,17 +45,18 @@ TRUSTED = (
     "pck/cuda/batched.py",  # the batched product's tree height, which sets tau
     "pck/cuda/gemv.py",
     "pck/cuda/_lib.py",  # the ctypes signatures of the ABI
-    "pck/_build.py",  # compiler flags: -ffp-contract=off, -fno-fast-math, no packed FP32
     "csrc/rounding.h",
     "csrc/check_pair.h",
+    "csrc/rowsum_check.h",
     "csrc/checker.hip",
     "csrc/bcheck.hip",
     "csrc/sampling.hip",
     "csrc/member.hip",
-    "csrc/gemv.hip",  # the tree whose height the b = 1 bound uses, and carried checks
+    "csrc/gemv.hip",  # the tree whose height the b = 1 bound uses; in-pass sums; carried checks
     "csrc/bgemm.hip",  # the batched product's order
     "../include/pck_hip.h",
 )
+
 THEOREMS = {
     "T1 no false alarms": "PCK.t1_block",
     "T2 guaranteed detection": "PCK.t2_block",
@@ -55,93 +64,146 @@ THEOREMS = {
     "T4 randomized detection": "PCK.t4_computed",
     "T4 spread errors": "PCK.t4_spread_computed",
 }
-"""What a GEMV certificate rests on (the reference's Lean names, lean/PCK/*.lean)."""
+"""The reference's Lean theorems a GEMV certificate rests on (lean/PCK/*.lean there)."""
 
 
 class CheckerMismatch(RuntimeError):
-    """The checker on disk is not the pinned one."""
+    """The trusted checker on disk, or its build settings, differ from the lock."""
 
 
-_HASHES: dict[Path, tuple[tuple[int, int], str]] = {}
+_DIGESTS: dict[Path, tuple[int, int, str]] = {}
 
 
-def _file_hash(path: Path) -> str:
-    """SHA-256 of a file, re-read only when its modification time or size changes."""
+def digest_file(path: Path) -> str:
+    """SHA-256 of a file, streamed; recomputed only when its size or modification time
+    changes (a proof-gated evaluation checks the pin before every episode)."""
     st = path.stat()
-    stamp = (st.st_mtime_ns, st.st_size)
-    cached = _HASHES.get(path)
-    if cached is None or cached[0] != stamp:
-        cached = (stamp, hashlib.sha256(path.read_bytes()).hexdigest())
-        _HASHES[path] = cached
-    return cached[1]
+    cached = _DIGESTS.get(path)
+    if cached is not None and cached[:2] == (st.st_size, st.st_mtime_ns):
+        return cached[2]
+    h = hashlib.sha256()
+    with path.open("rb") as f:
+        for chunk in iter(lambda: f.read(1 << 20), b""):
+            h.update(chunk)
+    _DIGESTS[path] = (st.st_size, st.st_mtime_ns, h.hexdigest())
+    return h.hexdigest()
 
 
-def file_hashes() -> dict[str, str]:
-    return {name: _file_hash((PACKAGE_ROOT / name).resolve()) for name in TRUSTED}
+def build_settings() -> dict[str, Any]:
+    """The compiler settings the thresholds assume, as the library is built."""
+    from pck import _build
+
+    return {
+        "arch": _build.ARCH,
+        "flags": list(_build.HIPCC_FLAGS),
+        "source_flags": {k: list(v) for k, v in sorted(_build.SOURCE_FLAGS.items())},
+    }
 
 
-def combined(hashes: dict[str, str]) -> str:
-    """One hash over (name, file hash) pairs in name order."""
-    text = "".join(f"{name}\0{digest}\n" for name, digest in sorted(hashes.items()))
-    return hashlib.sha256(text.encode()).hexdigest()
+def current_state() -> dict[str, Any]:
+    """Digests of the trusted files and the build settings, as the lock stores them."""
+    files = {name: digest_file(PACKAGE_ROOT / name) for name in TRUSTED}
+    return {"files": files, "build": build_settings()}
+
+
+def digest_state(state: dict[str, Any]) -> str:
+    """One digest over a state: canonical JSON (sorted keys, no whitespace) of files and
+    build settings."""
+    canonical = json.dumps(
+        {"files": state["files"], "build": state["build"]}, sort_keys=True, separators=(",", ":")
+    )
+    return hashlib.sha256(canonical.encode()).hexdigest()
 
 
 def checker_hash() -> str:
-    return combined(file_hashes())
+    """The digest a certificate quotes for the checker on disk."""
+    return digest_state(current_state())
 
 
 def pinned() -> dict[str, Any]:
+    """The lock: {"format", "checker", "files", "build"}."""
     data: dict[str, Any] = json.loads(LOCK.read_text())
     return data
 
 
+def differences(lock: dict[str, Any], state: dict[str, Any]) -> list[str]:
+    """Every trusted file and build setting on which ``state`` departs from ``lock``."""
+    out = []
+    names = sorted(set(lock.get("files", {})) | set(state["files"]))
+    out += [n for n in names if lock.get("files", {}).get(n) != state["files"].get(n)]
+    build = lock.get("build", {})
+    out += [f"build {k}" for k in sorted(state["build"]) if build.get(k) != state["build"][k]]
+    return out
+
+
 def verify_pinned() -> None:
-    """Raise `CheckerMismatch` naming the changed files if the checker is not the pinned one."""
+    """Raise `CheckerMismatch` naming what changed if the trusted checker on disk (files or
+    build settings) is not the pinned one."""
     lock = pinned()
-    if checker_hash() == lock["checker"]:
+    state = current_state()
+    changed = differences(lock, state)
+    if lock.get("format") != LOCK_FORMAT:
+        changed.append("lock format")
+    if not changed and digest_state(state) == lock.get("checker"):
         return
-    now = file_hashes()
-    changed = sorted(name for name in TRUSTED if lock["files"].get(name) != now[name])
+    changed = changed or ["lock digest"]
     raise CheckerMismatch(
-        f"trusted checker differs from the pinned one ({', '.join(changed)}); "
-        "review the change, then run: python -m pck.manifest --update"
+        f"trusted checker differs from the pinned one ({', '.join(changed)}); review the change, "
+        "then run: python -m pck.manifest --update"
     )
 
 
+def write_lock(path: Path | None = None) -> str:
+    """Pin the current state; returns its digest."""
+    state = current_state()
+    digest = digest_state(state)
+    lock = {"format": LOCK_FORMAT, "checker": digest, **state}
+    (path or LOCK).write_text(json.dumps(lock, indent=2, sort_keys=True) + "\n")
+    return digest
+
+
 def lean_hash() -> str | None:
-    """Hash of the Lean sources and build configuration (None where they are absent, as in
-    this build)."""
+    """Digest of the Lean sources and their build configuration under ``ROOT/lean`` (None
+    when there is no such directory, as in this build: its thresholds carry the reference's
+    theorems, which are not rebuilt here)."""
     lean = ROOT / "lean"
-    if not (lean / "lakefile.toml").exists():
+    if not lean.is_dir():
         return None
-    files = sorted(lean.glob("PCK/**/*.lean")) + [
-        lean / n for n in ("PCK.lean", "lakefile.toml", "lake-manifest.json", "lean-toolchain")
-    ]
-    h = hashlib.sha256()
-    for f in files:
-        h.update(str(f.relative_to(lean)).encode() + b"\0" + _file_hash(f).encode() + b"\0")
-    return h.hexdigest()
+    wanted = [p for p in sorted(lean.rglob("*")) if p.is_file() and (
+        p.suffix == ".lean" or p.name in ("lakefile.toml", "lake-manifest.json", "lean-toolchain")
+    ) and ".lake" not in p.parts]  # fmt: skip
+    listing = {str(p.relative_to(lean)): digest_file(p) for p in wanted}
+    return hashlib.sha256(json.dumps(listing, sort_keys=True).encode()).hexdigest()
 
 
-def git_commit() -> str | None:
-    return _git_commit(ROOT)
-
-
-@functools.cache
-def _git_commit(root: Path) -> str | None:
-    """HEAD of the checkout at ``root``, once per process."""
+def git_commit(root: Path | None = None) -> str | None:
+    """The commit checked out at ``root`` (default: the repository), read from ``.git``
+    directly (HEAD, a loose ref or packed-refs); None outside a checkout."""
+    git = (root or ROOT) / ".git"
     try:
-        out = subprocess.run(
-            ["git", "rev-parse", "HEAD"], cwd=root, capture_output=True, text=True, check=True
-        )
-    except (OSError, subprocess.CalledProcessError):
+        head = (git / "HEAD").read_text().strip()
+    except OSError:
         return None
-    return out.stdout.strip() or None
+    if not head.startswith("ref: "):
+        return head or None
+    ref = head[5:]
+    try:
+        return (git / ref).read_text().strip() or None
+    except OSError:
+        pass
+    try:
+        for line in (git / "packed-refs").read_text().splitlines():
+            parts = line.split()
+            if len(parts) == 2 and parts[1] == ref:
+                return parts[0]
+    except OSError:
+        pass
+    return None
 
 
 @dataclass(frozen=True)
 class Manifest:
-    """What one certified variant rests on (reference `manifest.py:132-159`)."""
+    """The certificate of one variant (the reference's fields, `src/pck/manifest.py:132-159`)."""
 
     task: str
     config: dict[str, Any]
@@ -161,31 +223,31 @@ class Manifest:
         return cls(**json.loads(text))
 
     def problems(self) -> list[str]:
-        """Why this manifest does not match the pinned checker and current proofs."""
+        """Why this certificate does not stand against the pinned checker and current proofs."""
         out = []
         if self.checker != pinned()["checker"]:
             out.append("checker hash differs from the pinned checker")
-        current = lean_hash()
-        if current is not None and self.lean != current:
+        lean = lean_hash()
+        if lean is not None and self.lean != lean:
             out.append("Lean sources differ from the ones the certificate was made with")
         return out
 
 
-def main() -> None:
-    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    parser.add_argument("--update", action="store_true", help="re-pin the current checker")
-    args = parser.parse_args()
-    hashes = file_hashes()
+def main(argv: list[str] | None = None) -> int:
+    parser = argparse.ArgumentParser(description="Pin or verify the trusted checker.")
+    parser.add_argument("--update", action="store_true", help="pin the checker on disk")
+    args = parser.parse_args(argv)
     if args.update:
-        LOCK.write_text(json.dumps({"checker": combined(hashes), "files": hashes}, indent=2) + "\n")
-        print(f"pinned {combined(hashes)}")
-        return
+        print(f"pinned {write_lock()}")
+        return 0
     try:
         verify_pinned()
-        print(f"checker matches the pin {checker_hash()}")
-    except CheckerMismatch as e:
-        print(e)
+    except CheckerMismatch as err:
+        print(err)
+        return 1
+    print(f"checker matches the pin {checker_hash()}")
+    return 0
 
 
 if __name__ == "__main__":
-    main()
+    raise SystemExit(main())
