@@ -81,33 +81,46 @@ def gemv_bytes(m: int, n: int, weight_bytes: int) -> int:
     return weight_bytes * m * n + 2 * n + 4 * m
 
 
+BLOCKS = (128, 256)  # checker block sizes measured (rows per checksum)
+
+
 def build_layers(copies: int, fp8: bool, gen):  # type: ignore[no-untyped-def]
+    """``copies`` layer copies; layer[name] = {"W", "x", "bank": {b: GpuBlockedChecker},
+    "rows": {b: RowSumChecker}} for each projection and checker block b."""
     import torch
 
-    from pck.cuda import GpuBlockedChecker, quantize_fp8
+    from pck.cuda import GpuBlockedChecker, RowSumChecker, quantize_fp8
     from pck.fp import tree_height
 
+    vec = 16 if fp8 else 8
     layers = []
     for _ in range(copies):
         layer = {}
         for name, m, n in LAYER:
-            W = (torch.randn(m, n, generator=gen) * 0.02).to(torch.bfloat16)
+            W = (torch.randn(m, n, generator=gen) * 0.02).to(torch.bfloat16).cuda()
             x = torch.randn(n, generator=gen).to(torch.bfloat16).cuda()
-            Wd = W.cuda()
             if fp8:
-                Q, _ = quantize_fp8(Wd)
-                checker = GpuBlockedChecker(Q.to(torch.bfloat16), BLOCK, tree_height(n, THREADS, 16), generator=gen)
-                layer[name] = (Q, x, checker)
-                del Wd
-            else:
-                checker = GpuBlockedChecker(Wd, BLOCK, tree_height(n, THREADS, 8), generator=gen)
-                layer[name] = (Wd, x, checker)
+                W = quantize_fp8(W)[0]
+            h = tree_height(n, THREADS, vec)
+            checked = W.to(torch.bfloat16) if fp8 else W  # FP8: the bound is on Q itself
+            layer[name] = {
+                "W": W,
+                "x": x,
+                "bank": {b: GpuBlockedChecker(checked, b, h, generator=gen) for b in BLOCKS},
+                "rows": {b: RowSumChecker(m, n, b, h, generator=gen) for b in BLOCKS},
+            }
+            del checked
         layers.append(layer)
     return layers
 
 
+def pairs(layer, names):  # type: ignore[no-untyped-def]
+    return [(layer[n]["W"], layer[n]["x"]) for n in names]
+
+
 def run_step(layer, with_check: bool, events=None):  # type: ignore[no-untyped-def]
-    """One decode layer; with ``events`` a list that receives (launch, start, end) per launch."""
+    """One decode layer; with ``with_check`` the seven outputs are checked by one standalone
+    bank-checker launch (b = 128); with ``events`` a list receiving (launch, start, end)."""
     import torch
 
     from pck.cuda import check_many, gemv_group
@@ -117,7 +130,7 @@ def run_step(layer, with_check: bool, events=None):  # type: ignore[no-untyped-d
         if events is not None:
             start = torch.cuda.Event(enable_timing=True)
             start.record()
-        ys = gemv_group([(layer[n][0], layer[n][1]) for n in names], THREADS)
+        ys = gemv_group(pairs(layer, names), THREADS)
         if events is not None:
             end = torch.cuda.Event(enable_timing=True)
             end.record()
@@ -127,7 +140,7 @@ def run_step(layer, with_check: bool, events=None):  # type: ignore[no-untyped-d
         if events is not None:
             start = torch.cuda.Event(enable_timing=True)
             start.record()
-        results = check_many([(layer[n][2], layer[n][1], outs[n]) for n, _, _ in LAYER])
+        results = check_many([(layer[n]["bank"][BLOCK], layer[n]["x"], outs[n]) for n, _, _ in LAYER])
         if events is not None:
             end = torch.cuda.Event(enable_timing=True)
             end.record()
@@ -136,13 +149,19 @@ def run_step(layer, with_check: bool, events=None):  # type: ignore[no-untyped-d
     return outs, None
 
 
-MODE_GEMV, MODE_SERIAL, MODE_OVERLAP, MODE_RIDE = "gemv", "serial", "overlapped", "carried"
-MODES = (MODE_GEMV, MODE_SERIAL, MODE_OVERLAP, MODE_RIDE)
+# Modes of the batch-1 pass.  gemv: the GEMVs alone.  serial / side_stream: one standalone
+# bank-checker launch per layer after its GEMVs, on the same stream / on a side stream
+# overlapping the next layer (the reference's modes).  carried: the bank checks ride in later
+# GEMV launches.  inpass: the GEMVs compute their row sums in the same pass and the row-sum
+# checks ride in later launches (no bank read).  inpass_sums: the in-pass GEMVs with no checks
+# (the cost of the sums alone).  A _b256 suffix: checker block b = 256 instead of 128.
+MODES = ("gemv", "serial", "side_stream", "carried", "carried_b256", "inpass", "inpass_b256",
+         "inpass_sums")  # fmt: skip
 
-# In carried mode the long launches of layer L also check outputs finished by earlier launches:
-# gate_up carries the previous layer's down and this layer's q, k, v, o; down carries gate and
-# up; the short q/k/v and o launches carry nothing (the pass ends with one standalone check of
-# the last down).  Each ("prev", name) entry refers to the previous layer's output.
+# In the carried and in-pass modes the long launches of layer L also check outputs finished by
+# earlier launches: gate_up carries the previous layer's down and this layer's q, k, v, o; down
+# carries gate and up; q/k/v and o carry nothing; the pass ends with one standalone check of
+# the last down.  ("prev", name) refers to the previous layer's output.
 CARRIES = {
     "qkv": (),
     "o": (),
@@ -151,76 +170,86 @@ CARRIES = {
 }
 
 
-def ride_pass(layers, depth: int):  # type: ignore[no-untyped-def]
-    """One decode pass of ``depth`` layers in carried mode; returns every check result."""
-    from pck.cuda import check_many, gemv_group_check
+def carried_pass(layers, depth: int, block: int, inpass: bool, checks: bool = True):  # type: ignore[no-untyped-def]
+    """One decode pass of ``depth`` layers whose checks ride in later launches: bank checks
+    (pck_gemv_group_check) or, with ``inpass``, row-sum checks of in-pass GEMVs
+    (pck_gemv_group_rowsums).  Returns every check result."""
+    from pck.cuda import check_many, gemv_group_check, gemv_group_rowsums, rowsum_check_many
 
     results = []
-    prev = None  # (layer, outputs) of the previous layer
+    prev = None  # (layer, outputs, sums) of the previous layer
     for i in range(depth):
         layer = layers[i % len(layers)]
-        outs = {}
+        outs, sums = {}, {}
         for launch, names in LAUNCHES:
-            checks = []
-            for which, name in CARRIES[launch]:
-                src = prev if which == "prev" else (layer, outs)
+            items = []
+            for which, name in CARRIES[launch] if checks else ():
+                src = prev if which == "prev" else (layer, outs, sums)
                 if src is not None:
-                    owner, produced = src
-                    checks.append((owner[name][2], owner[name][1], produced[name]))
-            ys, res = gemv_group_check([(layer[n][0], layer[n][1]) for n in names], checks, THREADS)
+                    owner, produced, produced_sums = src
+                    if inpass:
+                        items.append((owner[name]["rows"][block], produced_sums[name], produced[name]))
+                    else:
+                        items.append((owner[name]["bank"][block], owner[name]["x"], produced[name]))
+            if inpass:
+                ys, ss, res = gemv_group_rowsums(pairs(layer, names), items, THREADS)
+                sums.update(zip(names, ss))
+            else:
+                ys, res = gemv_group_check(pairs(layer, names), items, THREADS)
             results.extend(res)
             outs.update(zip(names, ys))
-        prev = (layer, outs)
-    owner, produced = prev
-    results.extend(check_many([(owner["down"][2], owner["down"][1], produced["down"])]))
+        prev = (layer, outs, sums)
+    if checks:
+        owner, produced, produced_sums = prev
+        if inpass:
+            results.extend(rowsum_check_many([(owner["down"]["rows"][block], produced_sums["down"], produced["down"])]))
+        else:
+            results.extend(check_many([(owner["down"]["bank"][block], owner["down"]["x"], produced["down"])]))
     return results
 
 
 def capture(layers, mode: str, depth: int):  # type: ignore[no-untyped-def]
-    """One HIP graph holding a decode pass of ``depth`` layers (cycling over the layer copies).
-
-    gemv:        the GEMV launches only;
-    serial:      each layer's checker launch follows its GEMVs on the same stream;
-    overlapped:  each layer's checker launch runs on a side stream once that layer's last GEMV
-                 has finished, concurrently with the next layer's GEMVs (the reference's
-                 SideStreamChecker pattern); the pass ends when the last check has.
-    Only this library's kernels are captured (no memset, no library reduction)."""
+    """One HIP graph holding a decode pass of ``depth`` layers (cycling over the layer copies)
+    in ``mode`` (see MODES).  Only this library's kernels are captured (no memset, no library
+    reduction).  Returns (graph, the pass's check results and outputs)."""
     import torch
 
     from pck.cuda import check_many
 
-    main = torch.cuda.current_stream()
-    side = torch.cuda.Stream()
-    warm = torch.cuda.Stream()
-    warm.wait_stream(main)
-    with torch.cuda.stream(warm):
-        for layer in layers:
-            run_step(layer, mode != MODE_GEMV)  # warm the allocator outside capture
-    main.wait_stream(warm)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    keep = []
-    if mode == MODE_RIDE:
-        with torch.cuda.graph(graph):
-            keep.append(ride_pass(layers, depth))
-        torch.cuda.synchronize()
-        return graph, keep
-    with torch.cuda.graph(graph):
+    def body():  # type: ignore[no-untyped-def]
+        if mode.startswith(("carried", "inpass")):
+            block = 256 if mode.endswith("_b256") else BLOCK
+            return carried_pass(layers, depth, block, mode.startswith("inpass"), mode != "inpass_sums")
+        keep = []
         cap = torch.cuda.current_stream()
         for i in range(depth):
             layer = layers[i % len(layers)]
-            outs, _ = run_step(layer, mode == MODE_SERIAL)
+            outs, res = run_step(layer, mode == "serial")
             keep.append(outs)
-            if mode == MODE_OVERLAP:
+            if res is not None:
+                keep.extend(res)
+            if mode == "side_stream":
                 ready = torch.cuda.Event()
                 ready.record(cap)
                 side.wait_event(ready)
                 with torch.cuda.stream(side):
-                    keep.append(check_many([(layer[n][2], layer[n][1], outs[n]) for n, _, _ in LAYER]))
-        if mode == MODE_OVERLAP:
+                    keep.extend(check_many([(layer[n]["bank"][BLOCK], layer[n]["x"], outs[n]) for n, _, _ in LAYER]))
+        if mode == "side_stream":
             done = torch.cuda.Event()
             done.record(side)
             cap.wait_event(done)
+        return keep
+
+    side = torch.cuda.Stream()
+    warm = torch.cuda.Stream()
+    warm.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(warm):
+        body()  # warm the allocator outside capture
+    torch.cuda.current_stream().wait_stream(warm)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        keep = body()
     torch.cuda.synchronize()
     return graph, keep
 
@@ -228,8 +257,7 @@ def capture(layers, mode: str, depth: int):  # type: ignore[no-untyped-def]
 def timed_modes(graphs: dict, depth: int, rounds: int) -> dict:  # type: ignore[type-arg]
     """ms per layer of each captured pass: one warm replay each, then ``rounds`` rounds that
     replay every pass once in turn; the median round per pass.  Alternating the passes gives
-    each the same clocks and cache state, which one back-to-back interval per pass, taken right
-    after its capture, did not."""
+    each the same clocks and cache state."""
     import torch
 
     for graph in graphs.values():
@@ -248,26 +276,59 @@ def timed_modes(graphs: dict, depth: int, rounds: int) -> dict:  # type: ignore[
     return {mode: statistics.median(t) for mode, t in times.items()}
 
 
-def dominant_launch_ms(layers, reps: int) -> tuple[float, int]:  # type: ignore[no-untyped-def]
-    """Mean duration of the dominant kernel's launches (q/k/v, o, gate/up groups) replayed
-    back to back from one graph over every layer copy, and their mean algorithmic bytes."""
+def honest_verdicts(keep) -> tuple[int, int]:  # type: ignore[no-untyped-def]
+    """(blocks checked, blocks rejected) over the CheckResults among ``keep``."""
+    from pck.cuda import CheckResult
+
+    results = [r for r in keep if isinstance(r, CheckResult)]
+    checked = sum(int(r.passed.numel()) for r in results)
+    rejected = sum(int((~r.passed).sum()) for r in results)
+    return checked, rejected
+
+
+def b1_modes(layers, depth: int, rounds: int) -> tuple[dict, dict]:  # type: ignore[no-untyped-def]
+    """ms per layer of every mode (alternating rounds) and the honest-run verdict counts."""
+    captured = {mode: capture(layers, mode, depth) for mode in MODES}
+    ms = timed_modes({mode: graph for mode, (graph, _) in captured.items()}, depth, rounds)
+    verdicts = {}
+    for mode, (_, keep) in captured.items():
+        checked, rejected = honest_verdicts(keep)
+        expect = 0 if mode in ("gemv", "inpass_sums") else 7 * depth
+        n_results = sum(1 for r in keep if hasattr(r, "passed"))
+        assert n_results == expect, (mode, n_results)
+        assert rejected == 0, f"{mode}: the checker rejected {rejected} honest blocks"
+        verdicts[mode] = checked
+    del captured
+    return ms, verdicts
+
+
+def dominant_launch_ms(layers, reps: int, inpass: bool = False) -> tuple[float, int]:  # type: ignore[no-untyped-def]
+    """Mean duration of the dominant kernel's launches (the q/k/v, o and gate/up groups; with
+    ``inpass`` the in-pass kernel, row sums included) replayed back to back from one graph over
+    every layer copy, timed with HIP events on the stream the launches run on, and their mean
+    algorithmic bytes."""
     import torch
 
-    from pck.cuda import gemv_group
+    from pck.cuda import gemv_group, gemv_group_rowsums
 
     dom = [launch for launch in LAUNCHES if launch[0] != "down"]
+
+    def launches() -> None:
+        for layer in layers:
+            for _, names in dom:
+                if inpass:
+                    gemv_group_rowsums(pairs(layer, names), (), THREADS)
+                else:
+                    gemv_group(pairs(layer, names), THREADS)
+
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        for layer in layers:
-            for _, names in dom:
-                gemv_group([(layer[n][0], layer[n][1]) for n in names], THREADS)
+        launches()
     torch.cuda.current_stream().wait_stream(side)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        for layer in layers:
-            for _, names in dom:
-                gemv_group([(layer[n][0], layer[n][1]) for n in names], THREADS)
+        launches()
     nbytes = sum(gemv_bytes(m, n, 2) for name, m, n in LAYER for _, names in dom if name in names)
     for _ in range(3):
         g.replay()
@@ -279,8 +340,7 @@ def dominant_launch_ms(layers, reps: int) -> tuple[float, int]:  # type: ignore[
         g.replay()
     end.record()
     torch.cuda.synchronize()
-    launches = len(dom) * len(layers)
-    return start.elapsed_time(end) / (reps * launches), nbytes // len(dom)
+    return start.elapsed_time(end) / (reps * len(dom) * len(layers)), nbytes // len(dom)
 
 
 def timed(layers, steps: int, warmup: int, with_check: bool, per_kernel: bool):  # type: ignore[no-untyped-def]
@@ -302,6 +362,112 @@ def timed(layers, steps: int, warmup: int, with_check: bool, per_kernel: bool): 
     for name, s, e in events or []:
         per_launch.setdefault(name, []).append(s.elapsed_time(e))
     return start.elapsed_time(end) / steps, per_launch
+
+
+def naive_shortcut(W, x, acc_bf16: bool = False, partial_bf16: bool = False):  # type: ignore[no-untyped-def]
+    """y = W x in the naive kernel's order (T = 256 lanes, lane t sums the contiguous chunk
+    [t c, (t + 1) c), then neighbour pairs) with one of the reference's planted shortcuts
+    (src/pck/gemv.py:14-57): the running sum rounded to BF16 after every add, or each lane's
+    chain sum rounded to BF16.  Torch ops on the GPU: the bench's fault generator."""
+    import torch
+
+    m, n = W.shape
+    lanes = 256
+    chunk = -(-n // lanes)
+    p = torch.zeros(m, lanes * chunk, device=W.device)
+    p[:, :n] = W.float() * x.float()
+    p = p.view(m, lanes, chunk)
+    acc = p[:, :, 0].clone()
+    for j in range(1, chunk):
+        acc = acc + p[:, :, j]
+        if acc_bf16:
+            acc = acc.bfloat16().float()
+    if partial_bf16:
+        acc = acc.bfloat16().float()
+    while acc.size(1) > 1:
+        acc = acc[:, 0::2] + acc[:, 1::2]
+    return acc[:, 0].contiguous()
+
+
+def planted_faults(W, x, y, gen):  # type: ignore[no-untyped-def]
+    """The reference campaign's faults for one GEMV output (harness/campaign.py:56-135):
+    a dropped reduction tail of 4 columns (the honest kernel on W with them zeroed), the BF16
+    accumulator and BF16 partials shortcuts, the BF16-rounded output, and one flip per block of
+    a random exponent bit (23-30) or of the sign bit of a random output."""
+    import torch
+
+    from pck.cuda import gemv_group
+
+    Wz = W.clone()
+    Wz.view(torch.uint8 if W.element_size() == 1 else torch.int16)[:, -4:] = 0
+    out = {
+        "drop_tail_4": gemv_group([(Wz, x)], THREADS)[0],
+        "bf16_accumulator": naive_shortcut(W, x, acc_bf16=True),
+        "bf16_partials": naive_shortcut(W, x, partial_bf16=True),
+        "bf16_output": y.bfloat16().float(),
+    }
+    blocks = y.numel() // BLOCK
+    base = torch.arange(0, y.numel(), BLOCK, device=y.device)
+    for kind, lo, hi in (("exponent_flip", 23, 31), ("sign_flip", 31, 32)):
+        rows = base + torch.randint(0, BLOCK, (blocks,), generator=gen).to(y.device)
+        bit = torch.randint(lo, hi, (blocks,), generator=gen).to(y.device)
+        z = y.clone()
+        zi = z.view(torch.int32)
+        zi[rows] ^= torch.bitwise_left_shift(torch.ones_like(bit, dtype=torch.int32), bit.int())
+        out[kind] = z
+    return out
+
+
+def fault_campaign_b1(layer, seed: int) -> dict:  # type: ignore[no-untyped-def]
+    """BASELINE config 4, reference-parity reading (batch 1), on one layer copy: each of the
+    seven outputs, honest and with every planted fault of `planted_faults`, checked by the bank
+    checker and by the row-sum checker of the in-pass path, at b = 128 and 256.  Per checker and
+    kind: outputs caught (some block rejected) of outputs, faulty blocks (y differs from the
+    honest output) caught, and false alarms (honest blocks rejected)."""
+    import torch
+
+    from pck.cuda import check_many, gemv_group_rowsums, rowsum_check_many
+
+    gen = torch.Generator().manual_seed(seed)
+    stats: dict = {}
+    honest_blocks = 0
+    for name, _, _ in LAYER:
+        ent = layer[name]
+        (y,), (sums,), _ = gemv_group_rowsums([(ent["W"], ent["x"])], (), THREADS)
+        cases = {"honest": y} | planted_faults(ent["W"], ent["x"], y, gen)
+        for b in BLOCKS:
+            bank, rows = ent["bank"][b], ent["rows"][b]
+            for kind, yy in cases.items():
+                faulty = (yy.view(-1, b) != y.view(-1, b)).any(dim=1)
+                for checker, res in (
+                    ("bank", check_many([(bank, ent["x"], yy)])[0]),
+                    ("rowsum", rowsum_check_many([(rows, sums, yy)])[0]),
+                ):
+                    v = res.verdict
+                    c = stats.setdefault(f"b{b}", {}).setdefault(checker, {}).setdefault(
+                        kind, {"outputs": 0, "outputs_caught": 0, "faulty_blocks": 0,
+                               "faulty_blocks_caught": 0, "false_alarms": 0})  # fmt: skip
+                    if kind == "honest":
+                        c["false_alarms"] += int((~v).sum())
+                        c["outputs"] += 1
+                        if b == BLOCK and checker == "bank":
+                            honest_blocks += v.numel()
+                        continue
+                    c["outputs"] += 1
+                    c["outputs_caught"] += int(bool((~v).any()))
+                    c["faulty_blocks"] += int(faulty.sum())
+                    c["faulty_blocks_caught"] += int((faulty & ~v).sum())
+                    c["false_alarms"] += int((~faulty & ~v).sum())
+    summary = {}
+    for bkey, per in stats.items():
+        for checker, kinds in per.items():
+            planted = {k: v for k, v in kinds.items() if k != "honest"}
+            summary[f"{checker}_{bkey}"] = {
+                "outputs_caught": f"{sum(v['outputs_caught'] for v in planted.values())}/"
+                                  f"{sum(v['outputs'] for v in planted.values())}",
+                "false_alarms": sum(v["false_alarms"] for v in kinds.values()),
+            }
+    return {"summary": summary, "by_kind": stats, "honest_blocks_b128": honest_blocks}
 
 
 def membership(copies: int = 4, reps: int = 20) -> dict:
@@ -759,6 +925,44 @@ def cpu_baseline(budget_s: float = 10.0, fp8: bool = False, all_cores: bool = Fa
     }
 
 
+def b1_section(fp8: bool, copies: int, depth: int, rounds: int, quick: bool, steps: int,
+               warmup: int, matched_ms: float) -> dict:  # fmt: skip
+    """The batch-1 decode layer for one weight type: every mode of MODES in alternating rounds,
+    the dominant kernels' launch durations (BF16), the eager per-launch times and the fault
+    campaign."""
+    import torch
+
+    gen = torch.Generator().manual_seed(1 if fp8 else 0)
+    kind = "FP8" if fp8 else "BF16"
+    print(f"[bench] building {copies} {kind} layer copies", file=sys.stderr, flush=True)
+    layers = build_layers(copies, fp8, gen)
+    nbytes = sum(gemv_bytes(m, n, 1 if fp8 else 2) for _, m, n in LAYER)
+    print(f"[bench] timing {kind} passes ({len(MODES)} modes, {rounds} rounds)", file=sys.stderr, flush=True)
+    ms, checked = b1_modes(layers, depth, rounds)
+    base = ms["gemv"]
+    out: dict = {
+        "gemv_only_gbps": round(nbytes / (base / 1e3) / 1e9, 1),
+        "gemv_only_ms": round(base, 5),
+        "modes_ms": {m: round(v, 5) for m, v in ms.items()},
+        "overhead_pct": {m: round(100 * (v / base - 1), 2) for m, v in ms.items() if m != "gemv"},
+        "honest_blocks_checked_per_pass": checked,
+        "gemv_only_pct_of_size_matched_read": round(100 * matched_ms / base, 2),
+    }
+    if not fp8:
+        reps = max(10, steps // 10)
+        out["dominant"] = dominant_launch_ms(layers, reps)
+        out["dominant_inpass"] = dominant_launch_ms(layers, reps, inpass=True)
+        if not quick:
+            ms_eager, per_launch = timed(layers, steps, warmup, True, per_kernel=True)
+            out["eager_ms_per_step"] = round(ms_eager, 5)
+            out["eager_launch_ms"] = {k: round(statistics.mean(v), 5) for k, v in per_launch.items()}
+    print(f"[bench] {kind} fault campaign (batch 1)", file=sys.stderr, flush=True)
+    out["faults"] = fault_campaign_b1(layers[0], seed=11 if fp8 else 10)
+    del layers
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> None:
     parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -768,15 +972,15 @@ def main() -> None:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument(
         "--quick", action="store_true",
-        help="one pass per mode, no eager timing, no CPU baseline (for counter collection)",
+        help="fewest rounds, no eager timing, no CPU baseline (for counter collection)",
     )  # fmt: skip
     parser.add_argument(
-        "--section", choices=("all", "templates"), default="all",
-        help="templates: time only the agent's GEMV templates and print that section",
+        "--section", choices=("all", "b1", "templates"), default="all",
+        help="b1: only the batch-1 layer (BF16 and FP8); templates: only the agent's templates",
     )  # fmt: skip
     args = parser.parse_args()
     if args.quick:
-        args.steps, args.warmup, args.no_cpu_baseline = 32, 1, True
+        args.warmup, args.no_cpu_baseline = 1, True
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the decode hot path "
               "here has no multi-GPU step", file=sys.stderr)  # fmt: skip
@@ -789,79 +993,60 @@ def main() -> None:
     if args.section == "templates":
         print(json.dumps({"templates": templates_layer()}), flush=True)
         return
+    depth = 32  # a Llama-3-8B decode pass
+    # At least 7 alternating rounds whatever --steps is; each round replays one 32-layer pass
+    # of every mode, so the medians never rest on one sample.
+    rounds = 3 if args.quick else max(7, args.steps // depth)
     bytes_bf16 = sum(gemv_bytes(m, n, 2) for _, m, n in LAYER)
-    launch_bytes = {
-        launch: sum(gemv_bytes(m, n, 2) for name, m, n in LAYER if name in names)
-        for launch, names in LAUNCHES
-    }
+    bytes_fp8 = sum(gemv_bytes(m, n, 1) for _, m, n in LAYER)
     # Read-only streams first, in a fresh address space like the layers' own: the long-stream
     # ceiling, and each launch's bytes read by one launch (what a launch of that size can reach).
     print("[bench] timing read-only streams", file=sys.stderr, flush=True)
     read_ceiling = read_bandwidth_gbps()
-    matched = dict(zip(launch_bytes, read_stream_ms(list(launch_bytes.values())), strict=True))
-    matched_ms = sum(matched.values())
-    launch_bytes8 = {
-        launch: sum(gemv_bytes(m, n, 1) for name, m, n in LAYER if name in names)
-        for launch, names in LAUNCHES
+    sizes = {w: {launch: sum(gemv_bytes(m, n, w) for name, m, n in LAYER if name in names)
+                 for launch, names in LAUNCHES} for w in (1, 2)}  # fmt: skip
+    matched = {w: dict(zip(sizes[w], read_stream_ms(list(sizes[w].values())), strict=True)) for w in (1, 2)}
+    torch.cuda.empty_cache()
+
+    common = dict(copies=args.copies, depth=depth, rounds=rounds, quick=args.quick,
+                  steps=args.steps, warmup=args.warmup)  # fmt: skip
+    b16 = b1_section(False, matched_ms=sum(matched[2].values()), **common)
+    b8 = b1_section(True, matched_ms=sum(matched[1].values()), **common)
+    detail: dict = {
+        "b1_bf16": b16,
+        "b1_fp8": b8,
+        "size_matched_read_us": {
+            kind: {k: round(1e3 * v, 2) for k, v in matched[w].items()}
+            for kind, w in (("bf16", 2), ("fp8", 1))
+        },
     }
-    matched8 = dict(zip(launch_bytes8, read_stream_ms(list(launch_bytes8.values())), strict=True))
-    matched8_ms = sum(matched8.values())
-    torch.cuda.empty_cache()
+    member = sampling = batched = templates = None
+    if args.section == "all":
+        print("[bench] timing the membership check", file=sys.stderr, flush=True)
+        member = membership()
+        print("[bench] timing the set-sampling checker", file=sys.stderr, flush=True)
+        sampling = sampling_checker(50 if args.quick else 200)
+        print("[bench] timing the batched layer (B = 128, 256)", file=sys.stderr, flush=True)
+        batched = batched_layer()
+        print("[bench] timing the agent's GEMV templates", file=sys.stderr, flush=True)
+        templates = templates_layer()
+        detail |= {"membership": member, "sampling": sampling, "batched": batched, "templates": templates}
 
-    gen = torch.Generator().manual_seed(0)
-    print(f"[bench] building {args.copies} BF16 layer copies", file=sys.stderr, flush=True)
-    bf16_layers = build_layers(args.copies, fp8=False, gen=gen)
-    # correctness first: every check passes on the honest outputs
-    _, results = run_step(bf16_layers[0], True)
-    args.steps = max(args.steps, 32)
-    assert all(bool(r.verdict.all()) for r in results), "checker rejected an honest output"
-
-    depth = 32  # a Llama-3-8B decode pass
-    reps = max(1, args.steps // depth)
-    print("[bench] timing BF16 passes (HIP graphs)", file=sys.stderr, flush=True)
-    captured = {mode: capture(bf16_layers, mode, depth) for mode in MODES}
-    ms = timed_modes({mode: graph for mode, (graph, _) in captured.items()}, depth, reps)
-    for mode in (MODE_OVERLAP, MODE_RIDE):
-        verdicts = [r for item in captured[mode][1] if isinstance(item, list) for r in item]
-        assert len(verdicts) == 7 * depth, len(verdicts)
-        assert all(bool(r.verdict.all()) for r in verdicts), "checker rejected an honest output"
-    del captured
-    ms_eager, per_launch = (float("nan"), {}) if args.quick else timed(
-        bf16_layers, args.steps, args.warmup, True, per_kernel=True
-    )
-    dom_ms, dom_bytes = dominant_launch_ms(bf16_layers, max(10, args.steps // 10))
-    del bf16_layers
-    torch.cuda.empty_cache()
-
-    print("[bench] building and timing FP8 passes", file=sys.stderr, flush=True)
-    fp8_layers = build_layers(args.copies, fp8=True, gen=gen)
-    _, results = run_step(fp8_layers[0], True)
-    assert all(bool(r.verdict.all()) for r in results), "checker rejected an honest FP8 output"
-    bytes_fp8 = sum(gemv_bytes(m, n, 1) for _, m, n in LAYER)
-    captured = {mode: capture(fp8_layers, mode, depth) for mode in MODES}
-    ms8 = timed_modes({mode: graph for mode, (graph, _) in captured.items()}, depth, reps)
-    for mode in (MODE_OVERLAP, MODE_RIDE):
-        verdicts = [r for item in captured[mode][1] if isinstance(item, list) for r in item]
-        assert len(verdicts) == 7 * depth, len(verdicts)
-        assert all(bool(r.verdict.all()) for r in verdicts), "checker rejected an honest output"
-    del captured
-    del fp8_layers
-    torch.cuda.empty_cache()
-    ms_checked, ms_gemv_only = ms[MODE_RIDE], ms[MODE_GEMV]
-    fp8_checked, fp8_gemv_only = ms8[MODE_RIDE], ms8[MODE_GEMV]
-
-    print("[bench] timing the membership check", file=sys.stderr, flush=True)
-    member = membership()
-    print("[bench] timing the set-sampling checker", file=sys.stderr, flush=True)
-    sampling = sampling_checker(50 if args.quick else 200)
-    print("[bench] timing the batched layer (B = 128, 256)", file=sys.stderr, flush=True)
-    batched = batched_layer()
-    print("[bench] timing the agent's GEMV templates", file=sys.stderr, flush=True)
-    templates = templates_layer()
-    achieved = dom_bytes / (dom_ms / 1e3) / 1e9
+    # The headline: the batch-1 BF16 layer with every output checked, in the fastest checked
+    # mode (bank checks carried in later GEMV launches, b = 128).
+    ms_checked = b16["modes_ms"]["carried"]
     value = bytes_bf16 / (ms_checked / 1e3) / 1e9
+    dom_ms, dom_bytes = b16["dominant"]
+    achieved = dom_bytes / (dom_ms / 1e3) / 1e9
 
-    line = {
+    def ovh(sec: dict) -> dict:
+        o = sec["overhead_pct"]
+        return {"inpass_b128": o["inpass"], "inpass_b256": o["inpass_b256"],
+                "bank_carried_b128": o["carried"], "bank_carried_b256": o["carried_b256"],
+                "bank_serial_b128": o["serial"], "bank_side_stream_b128": o["side_stream"],
+                "inpass_sums_only": o["inpass_sums"]}  # fmt: skip
+
+    line: dict = {
         "metric": "GEMV HBM GB/s (% of peak), BF16/FP8, Llama-3-8B shapes; checker overhead %",
         "value": round(value, 1),
         "unit": "GB/s",
@@ -879,54 +1064,59 @@ def main() -> None:
             "output checked by the blocked checker (b=128, K=1, T=256) in a later launch of the "
             "pass; 32-layer passes replayed from a HIP graph",
             "layer_copies": args.copies,
+            "rounds": rounds,
             "gemv_bytes_per_step": bytes_bf16,
         },
         "pct_of_peak": round(100 * value / HBM_PEAK_GBPS, 2),
-        "gemv_only_gbps": round(bytes_bf16 / (ms_gemv_only / 1e3) / 1e9, 1),
-        "checker_overhead_pct": round(100 * (ms_checked / ms_gemv_only - 1), 2),
-        "checker_overhead_serial_pct": round(100 * (ms[MODE_SERIAL] / ms_gemv_only - 1), 2),
-        "checker_overhead_side_stream_pct": round(100 * (ms[MODE_OVERLAP] / ms_gemv_only - 1), 2),
-        "eager_ms_per_step": None if args.quick else round(ms_eager, 5),
-        "fp8": {
-            "value_gbps": round(bytes_fp8 / (fp8_checked / 1e3) / 1e9, 1),
-            "gemv_only_gbps": round(bytes_fp8 / (fp8_gemv_only / 1e3) / 1e9, 1),
-            "checker_overhead_pct": round(100 * (fp8_checked / fp8_gemv_only - 1), 2),
-            "checker_overhead_serial_pct": round(100 * (ms8[MODE_SERIAL] / fp8_gemv_only - 1), 2),
-            "checker_overhead_side_stream_pct": round(
-                100 * (ms8[MODE_OVERLAP] / fp8_gemv_only - 1), 2
-            ),
-            "ms_per_step": round(fp8_checked, 5),
-            "size_matched_read_us": {k: round(1e3 * v, 2) for k, v in matched8.items()},
-            "pct_of_size_matched_read": round(100 * matched8_ms / fp8_checked, 2),
-            "gemv_only_pct_of_size_matched_read": round(100 * matched8_ms / fp8_gemv_only, 2),
-        },
-        "eager_launch_ms": {k: round(statistics.mean(v), 5) for k, v in per_launch.items()},
-        "hbm_read_ceiling_gbps": round(read_ceiling, 1),
+        "gemv_only_gbps": b16["gemv_only_gbps"],
         "pct_of_read_ceiling": round(100 * value / read_ceiling, 2),
-        "size_matched_read_us": {k: round(1e3 * v, 2) for k, v in matched.items()},
-        "pct_of_size_matched_read": round(100 * matched_ms / ms_checked, 2),
-        "gemv_only_pct_of_size_matched_read": round(100 * matched_ms / ms_gemv_only, 2),
-        "membership": member,
-        "sampling": sampling,
-        "batched": batched,
-        "templates": templates,
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "gemv_tree_kernel<256,1,2,bf16,nt> (q/k/v, o, gate/up launches)",
-            "launch_ms": round(dom_ms, 5),
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": recorded_traffic(),
-            "traffic_source": TRAFFIC_PROFILE.relative_to(ROOT).as_posix(),
+        "hbm_read_ceiling_gbps": round(read_ceiling, 1),
+        "pct_of_size_matched_read": round(100 * sum(matched[2].values()) / ms_checked, 2),
+        "fp8": {
+            "value_gbps": round(bytes_fp8 / (b8["modes_ms"]["carried"] / 1e3) / 1e9, 1),
+            "gemv_only_gbps": b8["gemv_only_gbps"],
+            "ms_per_step": b8["modes_ms"]["carried"],
+            "pct_of_size_matched_read": round(100 * sum(matched[1].values()) / b8["modes_ms"]["carried"], 2),
         },
+        "checker_overhead_pct": ovh(b16),
+        "fp8_checker_overhead_pct": ovh(b8),
+        "faults_b1": {"bf16": b16["faults"]["summary"], "fp8": b8["faults"]["summary"]},
+    }
+    if member is not None:
+        line["membership"] = {k: member[k] for k in ("ms", "gbps", "pct_of_peak", "planted_caught", "false_alarms")}
+    if batched is not None:
+        line["batched"] = {
+            key: {w: {"products_ms": e[w]["gemm_only_ms"], "checker_overhead_pct": e[w]["checker_overhead_pct"],
+                      "mfma_peak_frac": e[w]["mfma_peak_frac"],
+                      "faulty_columns_caught": f"{e[w]['faulty_columns_caught']}/{e[w]['faulty_columns']}",
+                      "false_alarms": e[w]["false_alarms"]} for w in ("bf16", "fp8")}
+                 | {"hipblaslt_ms": e["hipblaslt_ms_per_layer"]}
+            for key, e in batched.items()
+        }  # fmt: skip
+    line["roofline"] = {
+        "bound": "hbm",
+        "kernel": "gemv_tree_kernel<256,1,2,bf16,nt> (q/k/v, o, gate/up launches)",
+        "launch_ms": round(dom_ms, 5),
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBPS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBPS, 4),
+        "traffic": recorded_traffic(),
+        "traffic_source": TRAFFIC_PROFILE.relative_to(ROOT).as_posix(),
+        "inpass_kernel_launch_ms": round(b16["dominant_inpass"][0], 5),
+        "inpass_kernel_frac": round(dom_bytes / (b16["dominant_inpass"][0] / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
     }
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU baselines", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline()
-        line["cpu_baseline_all_cores"] = cpu_baseline(all_cores=True)
-        line["fp8"]["cpu_baseline"] = cpu_baseline(fp8=True)
+        detail["cpu_baseline_all_cores"] = cpu_baseline(all_cores=True)
+        detail["fp8_cpu_baseline"] = cpu_baseline(fp8=True)
+        line["cpu_baseline_all_cores_gbps"] = detail["cpu_baseline_all_cores"]["value"]
+        line["fp8_cpu_baseline_gbps"] = detail["fp8_cpu_baseline"]["value"]
+        if member is not None:
+            line["membership"]["cpu_baseline_gbps"] = member["cpu_baseline"]["value"]
+    # the full per-section figures go to stderr (one JSON line), the contract line to stdout
+    print("[bench detail] " + json.dumps(detail), file=sys.stderr, flush=True)
     print(json.dumps(line), flush=True)
 
 

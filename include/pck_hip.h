@@ -83,6 +83,8 @@ int pck_gemv_group_check(int weight_kind, const PckGemv* gemvs, int count, int t
  * counterpart. */
 int pck_gemv_set_shape(int rows_per_wave, int unroll, int nontemporal);
 
+
+
 /* ---------------------------------------------------------------------------------------------
  * Batched decode product Y (batch, m) FP32 = X (batch, n) BF16 times W^T, W (m, n) BF16
  * (weight_kind 0) or E4M3FN codes (weight_kind 1), on the matrix cores.  Each
@@ -161,21 +163,23 @@ int pck_blocked_check(const PckCheckBatch* batch, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * In-pass checksums: the blocked check without a bank.  A GEMV launch that also writes, for
- * every output row i, the FP64 pair (d_i, s_i) from the weights it streams anyway:
- *   d_i = sum_j W_ij x_j      each product exact (one FMA per term, round to nearest)
- *   s_i = sum_j |W_ij x_j|    the same with absolute values
- * Lane l of the row's min(threads, 64) lanes adds its columns in the tree's own order
- * (vector positions, then chains l, l + 64, ..., then the columns of a vector), starting
- * from +0; the lanes then combine by an xor butterfly (offsets 32 .. 1, or 16 .. 1 at
- * threads = 32).  The rows' y keep the bits of pck_gemv_group.
+ * every output row i, an FP64 pair from the FP32 products p_j = W_ij x_j its tree forms anyway:
+ *   d_i  consecutive products added in pairs in FP32, the pair sums widened and added in FP64
+ *   s_i  sum_j |p_j| in FP32 (stored widened)
+ * Lane l of the row's min(threads, 64) lanes keeps one (d, s) per chain (l, l + 64, ...),
+ * from +0, and takes each chain's columns in the tree's own order (vector positions, then the
+ * columns of a vector); the chains combine in halving order (chain i += chain i + half), then
+ * the lanes by an xor butterfly (offsets 32 .. 1, or 16 .. 1 at threads = 32).  The rows' y
+ * keep the bits of pck_gemv_group.
  * A row-sum check then needs only (d, s), y and the signs of each block:
  *   rho = sum_i r_i d_i - sum_i r_i y_i                       FP64, round to nearest
- *   s   = s_factor * sum_i s_i, rounded up, then up to FP32    (s_factor bounds the RN sums)
+ *   s   = s_factor * sum_i s_i, rounded up, then up to FP32    (s_factor bounds the FP32 sums)
  *   tau = coef s + geps ((1 + u32) s + sum |y_i|) + tau_floor  every operation rounded up
  * and the block passes only if its y are finite, tau is finite and |rho| <= tau: the blocked
  * checker's relation (reference src/pck/cuda/csrc/checker_kernel.cu:115-183) with c . x
- * replaced by r^T (W x) evaluated from exact products and s = a . |x| by its exact value
- * (never above the bank's BF16 bound), so the threshold stays sound and is never looser.
+ * replaced by r^T (W x) from the pair sums (their FP32 rounding, at most u32 sum |p|, is the
+ * budget coef's u32 term gives c's FP32 rounding there) and s = a . |x| by a bound on the exact
+ * sum of |W_ij x_j| (the bank's a carries BF16 rounding up to 2^-8 on top).
  * One wave per (check, block) pair: lane l takes rows l, l + 64, ... in order, then an xor
  * butterfly (cx and r.y round to nearest, s and sum |y| round up).  No reference
  * counterpart: the reference always reads a precomputed bank (src/pck/cuda/checker.py:91-104),
@@ -194,9 +198,9 @@ typedef struct PckRowSumCheckDesc {
   int32_t reserved;   /* 0 */
   double coef;        /* >= gamma_h + u32, rounded up                                    */
   double geps;        /* >= gamma_H(u64), H >= D + ceil(b / 64) + 7                      */
-  double tau_floor;   /* >= n 2^-148                                                     */
-  double s_factor;    /* >= 1 / (1 - D 2^-53), D >= the row sums' depth: the max over    */
-                      /* threads T and vector width V of                                  */
+  double tau_floor;   /* >= n 2^-148 + 2 b n 2^-150 (FP32 product underflow)             */
+  double s_factor;    /* >= 1 / (1 - gamma_D(u32)), D >= the row sums' depth: the max    */
+                      /* over threads T and vector width V of                             */
                       /* (T / min(T, 64)) ceil(ceil(n / V) / T) V + log2 min(T, 64)       */
 } PckRowSumCheckDesc;
 

@@ -1,13 +1,14 @@
 """TEST INFRASTRUCTURE — CPU model of the in-pass checksums and the row-sum check.
 
-The in-pass GEMV writes, beside y = W x, one FP64 pair per output row,
+The in-pass GEMV writes, beside y = W x, one pair per output row from the FP32 products
+p_j = fl32(W_ij x_j) the tree forms anyway (exact barring FP32 underflow):
 
-    d_i = sum_j W_ij x_j        s_i = sum_j |W_ij x_j|,
+    d_i = sum over consecutive pairs (p_2k + p_2k+1), each pair added in FP32, the pair sums
+          widened and added in FP64 (round to nearest);
+    s_i = sum_j |p_j| in FP32 (round to nearest), stored widened to FP64.
 
-each product exact (BF16 x BF16 and E4M3 x BF16 products have at most 16 significand bits and
-never underflow in FP64) and every addition rounded to nearest.  The row-sum check then
-decides every (check, block) pair of the blocked checker (reference relation
-`src/pck/cuda/csrc/checker_kernel.cu:115-183`, bank quantities replaced):
+The row-sum check then decides every (check, block) pair of the blocked checker (reference
+relation `src/pck/cuda/csrc/checker_kernel.cu:115-183`, bank quantities replaced):
 
     rho = sum_i r_i d_i - sum_i r_i y_i
     s   = up_to_f32(RU(s_factor * RU(sum_i s_i)))
@@ -15,11 +16,12 @@ decides every (check, block) pair of the blocked checker (reference relation
     passed = every y_i finite and tau finite and |rho| <= tau.
 
 `row_sums` and `rowsum_check_with_signs` reproduce the GPU's bits: the same summation order
-(lane l of a row's L = min(T, 64) lanes adds vector positions, then chains, then the columns of
-each vector; an xor butterfly across lanes; the check's lane l adds rows l, l + 64, ... and an
-xor butterfly) and the same directed-rounding steps (error-free transformations plus a one-ulp
-raise, as the library's device code forms them).  `exact_rowsum_threshold` is the same
-threshold in exact rational arithmetic, against which the rounded one is pinned.
+(lane l of a row's L = min(T, 64) lanes takes vector positions, then chains, then the columns
+of each vector in order; an xor butterfly across lanes; the check's lane l adds rows l, l + 64,
+... and an xor butterfly) and the same directed-rounding steps (error-free transformations plus
+a one-ulp raise, as the library's device code forms them).  `exact_rowsum_threshold` is the
+threshold for the exact S = sum |W_ij x_j| in rational arithmetic, against which the rounded
+one is pinned.
 """
 
 from __future__ import annotations
@@ -44,16 +46,20 @@ def depth_of(n: int, threads: int, vec: int) -> int:
 
 
 def rowsum_constants(n: int, block: int, height: int) -> dict[str, float]:
-    """coef, geps, tau_floor and s_factor of a row-sum check (the host's formulas): coef and
-    tau_floor as the bank checker's (reference `src/pck/cuda/checker.py:106-125`); with D the
-    largest `depth_of` over thread counts 32..1024 and vectors of 8 and 16, s_factor =
-    1 + (D + 1) 2^-52 >= 1 / (1 - D u64) and geps = gamma_H(u64), H = D + ceil(b / 64) + 7."""
+    """coef, geps, tau_floor and s_factor of a row-sum check (the host's formulas).  coef is
+    the bank checker's gamma_h + u32 (reference `src/pck/cuda/checker.py:106-125`): its u32 term
+    covered c's FP32 rounding there and covers the FP32 pair sums of d here (at most
+    u32 sum |p| per row).  With D the largest `depth_of` over thread counts 32..1024 and
+    vectors of 8 and 16: s_factor = 1 + (D + 1) 2^-23 >= 1 / (1 - gamma_D(u32)) bounds the FP32
+    sums of |p|; geps = gamma_H(u64), H = D + ceil(b / 64) + 7, bounds rho's FP64 evaluation;
+    tau_floor = n 2^-148 + 2 b n 2^-150 adds what FP32 product underflow may take from d and
+    s (at most 2^-150 per product)."""
     D = max(depth_of(n, t, v) for t in (32, 64, 128, 256, 512, 1024) for v in (8, 16))
     return {
         "coef": next_up(gamma(height) + U32, 2),
         "geps": next_up(gamma(D + -(-block // WAVE) + 7, U64), 2),
-        "tau_floor": next_up(n * 2.0**-148, 2),
-        "s_factor": next_up(1.0 + (D + 1) * 2.0**-52, 2),
+        "tau_floor": next_up(n * 2.0**-148 + 2 * block * n * 2.0**-150, 2),
+        "s_factor": next_up(1.0 + (D + 1) * 2.0**-23, 2),
     }
 
 
@@ -65,10 +71,12 @@ def row_sums(
 
     ``W`` holds the weight values (BF16 or decoded E4M3) and ``x`` the BF16 activations, as
     floats; ``vec`` is 8 for BF16 weights and 16 for E4M3.  Lane l of L = min(threads, 64)
-    owns the chains t = l + L j (j < threads / L) of the coalesced tree; it adds, for each
-    vector position v, for each chain j, the ``vec`` products of vector v threads + t in column
-    order (columns past n count as +0), starting from +0.  Then for off = L/2, ..., 1 every lane
-    adds its partner's value (lane ^ off).
+    owns the chains t = l + L j (j < C = threads / L) of the coalesced tree, each with its own
+    d (FP64) and s (FP32), from +0; for each vector position v, for each chain j, it takes the
+    ``vec`` products of vector v threads + t (FP32, columns past n as +0) and adds, pair by pair,
+    fl32(p_k + p_k+1) to d_j and |p_k| then |p_k+1| to s_j.  The chains combine in halving
+    order (for half = C/2, ..., 1: chain i += chain i + half), then for off = L/2, ..., 1 every
+    lane adds its partner's d and s (lane ^ off), in FP64 and FP32.
     """
     m, n = W.shape
     lanes = min(threads, WAVE)
@@ -76,29 +84,37 @@ def row_sums(
     per_lane = -(-(-(-n // vec)) // threads)
     width = per_lane * threads * vec
     lane_idx = np.arange(lanes)
-    xs = np.zeros(width)
-    xs[:n] = np.asarray(x, dtype=np.float64)
+    xs = np.zeros(width, dtype=np.float32)
+    xs[:n] = np.asarray(x, dtype=np.float32)
     out = np.empty((m, 2))
-    for r0 in range(0, m, chunk_rows):
-        Wc = np.zeros((min(chunk_rows, m - r0), width))
-        Wc[:, :n] = W[r0 : r0 + chunk_rows]
-        p = Wc * xs  # exact: at most 16 significand bits, no FP64 underflow
-        d = np.zeros((p.shape[0], lanes))
-        s = np.zeros((p.shape[0], lanes))
-        for v in range(per_lane):
-            for j in range(chains):
-                base = (v * threads + lanes * j + lane_idx) * vec
-                for k in range(vec):
-                    col = p[:, base + k]
-                    d = d + col
-                    s = s + np.abs(col)
-        off = lanes // 2
-        while off > 0:
-            d = d + d[:, lane_idx ^ off]
-            s = s + s[:, lane_idx ^ off]
-            off //= 2
-        out[r0 : r0 + p.shape[0], 0] = d[:, 0]
-        out[r0 : r0 + p.shape[0], 1] = s[:, 0]
+    with np.errstate(under="ignore", over="ignore", invalid="ignore"):
+        for r0 in range(0, m, chunk_rows):
+            Wc = np.zeros((min(chunk_rows, m - r0), width), dtype=np.float32)
+            Wc[:, :n] = W[r0 : r0 + chunk_rows]
+            p = Wc * xs  # FP32 products, as the tree forms them
+            d = np.zeros((chains, p.shape[0], lanes))
+            s = np.zeros((chains, p.shape[0], lanes), dtype=np.float32)
+            for v in range(per_lane):
+                for j in range(chains):
+                    base = (v * threads + lanes * j + lane_idx) * vec
+                    for k in range(0, vec, 2):
+                        p0, p1 = p[:, base + k], p[:, base + k + 1]
+                        d[j] = d[j] + (p0 + p1).astype(np.float64)
+                        s[j] = s[j] + np.abs(p0)
+                        s[j] = s[j] + np.abs(p1)
+            half = chains // 2
+            while half > 0:  # chain i += chain i + half
+                d[:half] = d[:half] + d[half : 2 * half]
+                s[:half] = s[:half] + s[half : 2 * half]
+                half //= 2
+            d, s = d[0], s[0]
+            off = lanes // 2
+            while off > 0:
+                d = d + d[:, lane_idx ^ off]
+                s = s + s[:, lane_idx ^ off]
+                off //= 2
+            out[r0 : r0 + p.shape[0], 0] = d[:, 0]
+            out[r0 : r0 + p.shape[0], 1] = s[:, 0].astype(np.float64)
     return out
 
 

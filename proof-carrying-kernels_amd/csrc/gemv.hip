@@ -70,20 +70,21 @@ __device__ __forceinline__ float2 fp8_pair(uint32_t w) {
 
 __device__ __forceinline__ float fp8_one(uint8_t code) { return fp8_pair<false>(code).x; }
 
-// Row sums of the in-pass path: d += w x and s += |w| |x| in FP64, each product exact (8 + 8 or
-// 4 + 8 significand bits, never underflowing in FP64), one rounding per term (the FMA's).
+// Row sums of the in-pass path, from the FP32 products the tree already forms (exact: 8 + 8 or
+// 4 + 8 significand bits, barring FP32 underflow).  Each pair of consecutive products is added
+// in FP32 (rounding error at most u32 (|p0| + |p1|)), widened and added to d in FP64; |p| is
+// added to s in FP32, one product at a time in column order.
 struct RowSums {
   double d = 0.0;
-  double s = 0.0;
+  float s = 0.0f;
 };
 
 template <bool kSums>
-__device__ __forceinline__ void add_sums(RowSums& rs, float w, float x) {
+__device__ __forceinline__ void add_pair(RowSums& rs, float p0, float p1) {
   if constexpr (kSums) {
-    const double wd = static_cast<double>(w);
-    const double xd = static_cast<double>(x);
-    rs.d = __builtin_fma(wd, xd, rs.d);
-    rs.s = __builtin_fma(__builtin_fabs(wd), __builtin_fabs(xd), rs.s);
+    rs.d = rs.d + static_cast<double>(p0 + p1);
+    rs.s = rs.s + __builtin_fabsf(p0);
+    rs.s = rs.s + __builtin_fabsf(p1);
   }
 }
 
@@ -96,14 +97,11 @@ __device__ __forceinline__ void add_products(float& acc, RowSums& rs, const uint
     const uint32_t xd[4] = {xa.x, xa.y, xa.z, xa.w};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const float w0 = bf16_lo(wd[k]), x0 = bf16_lo(xd[k]);
-      const float w1 = bf16_hi(wd[k]), x1 = bf16_hi(xd[k]);
-      const float p0 = w0 * x0;
-      const float p1 = w1 * x1;
+      const float p0 = bf16_lo(wd[k]) * bf16_lo(xd[k]);
+      const float p1 = bf16_hi(wd[k]) * bf16_hi(xd[k]);
       acc = acc + p0;
       acc = acc + p1;
-      add_sums<kSums>(rs, w0, x0);
-      add_sums<kSums>(rs, w1, x1);
+      add_pair<kSums>(rs, p0, p1);
     }
   } else {
     const uint32_t xd[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
@@ -111,20 +109,16 @@ __device__ __forceinline__ void add_products(float& acc, RowSums& rs, const uint
     for (int k = 0; k < 4; ++k) {
       const float2 f01 = fp8_pair<false>(wd[k]);
       const float2 f23 = fp8_pair<true>(wd[k]);
-      const float x0 = bf16_lo(xd[2 * k]), x1 = bf16_hi(xd[2 * k]);
-      const float x2 = bf16_lo(xd[2 * k + 1]), x3 = bf16_hi(xd[2 * k + 1]);
-      const float p0 = f01.x * x0;
-      const float p1 = f01.y * x1;
-      const float p2 = f23.x * x2;
-      const float p3 = f23.y * x3;
+      const float p0 = f01.x * bf16_lo(xd[2 * k]);
+      const float p1 = f01.y * bf16_hi(xd[2 * k]);
+      const float p2 = f23.x * bf16_lo(xd[2 * k + 1]);
+      const float p3 = f23.y * bf16_hi(xd[2 * k + 1]);
       acc = acc + p0;
       acc = acc + p1;
       acc = acc + p2;
       acc = acc + p3;
-      add_sums<kSums>(rs, f01.x, x0);
-      add_sums<kSums>(rs, f01.y, x1);
-      add_sums<kSums>(rs, f23.x, x2);
-      add_sums<kSums>(rs, f23.y, x3);
+      add_pair<kSums>(rs, p0, p1);
+      add_pair<kSums>(rs, p2, p3);
     }
   }
 }
@@ -135,23 +129,25 @@ template <bool kFp8, bool kSums = false>
 __device__ __forceinline__ void add_products_scalar(float& acc, RowSums& rs, const void* w_row,
                                                     const uint16_t* x, int64_t col, int64_t n) {
   constexpr int V = kFp8 ? 16 : 8;
+  float p[V];
 #pragma unroll
   for (int k = 0; k < V; ++k) {
     const int64_t j = col + k;
-    float p = 0.0f;
-    float wv = 0.0f, xv = 0.0f;
+    p[k] = 0.0f;
     if (j < n) {
-      xv = __uint_as_float(static_cast<uint32_t>(x[j]) << 16);
+      const float xv = __uint_as_float(static_cast<uint32_t>(x[j]) << 16);
+      float wv;
       if constexpr (kFp8) {
         wv = fp8_one(static_cast<const uint8_t*>(w_row)[j]);
       } else {
         wv = __uint_as_float(static_cast<uint32_t>(static_cast<const uint16_t*>(w_row)[j]) << 16);
       }
-      p = wv * xv;
+      p[k] = wv * xv;
     }
-    acc = acc + p;
-    add_sums<kSums>(rs, wv, xv);
+    acc = acc + p[k];
   }
+#pragma unroll
+  for (int k = 0; k < V; k += 2) add_pair<kSums>(rs, p[k], p[k + 1]);
 }
 
 // a[i] += a[i + 16] ... a[0] += a[1] inside each 32-lane half of the wave, the halving order of
@@ -232,7 +228,7 @@ __device__ __forceinline__ void gemv_rows(const GemvBatch& batch, int64_t group)
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int j = 0; j < kChains; ++j) acc[r][j] = -0.0f;
-  RowSums rs[R];  // per row: one FP64 pair per lane over all of its chains (kSums only)
+  RowSums rs[R][kChains];  // per row and chain: the lane's d and s (kSums only)
 
   for (int64_t v0 = 0; v0 < P; v0 += U) {
     if constexpr (kVector) {
@@ -268,7 +264,7 @@ __device__ __forceinline__ void gemv_rows(const GemvBatch& batch, int64_t group)
         for (int r = 0; r < R; ++r)
 #pragma unroll
           for (int j = 0; j < kChains; ++j)
-            add_products<kFp8, kSums>(acc[r][j], rs[r], wb[u][r][j], xa[u][j],
+            add_products<kFp8, kSums>(acc[r][j], rs[r][j], wb[u][r][j], xa[u][j],
                                       kFp8 ? xb[u][j] : xa[u][j]);
       }
     } else {
@@ -277,27 +273,36 @@ __device__ __forceinline__ void gemv_rows(const GemvBatch& batch, int64_t group)
 #pragma unroll
         for (int j = 0; j < kChains; ++j) {
           const int64_t col = (v0 * T + chain0 + kLanesPerRow * j) * V;
-          add_products_scalar<kFp8, kSums>(acc[r][j], rs[r], w_rows[r], x, col, n);
+          add_products_scalar<kFp8, kSums>(acc[r][j], rs[r][j], w_rows[r], x, col, n);
         }
       }
     }
   }
 
   if constexpr (kSums) {
-    // The row's lanes combine their FP64 pairs by an xor butterfly (symmetric, so every lane of
-    // the row ends with the same pair); the row's first lane stores it as one 16-byte write.
+    // Each lane combines its chains' sums in halving order (chain i += chain i + half), then
+    // the row's lanes combine theirs by an xor butterfly (symmetric, so every lane of the row
+    // ends with the same pair); the row's first lane stores it as one 16-byte write.
 #pragma unroll
     for (int r = 0; r < R; ++r) {
 #pragma unroll
+      for (int half = kChains / 2; half > 0; half /= 2)
+#pragma unroll
+        for (int i = 0; i < half; ++i) {
+          rs[r][i].d = rs[r][i].d + rs[r][i + half].d;
+          rs[r][i].s = rs[r][i].s + rs[r][i + half].s;
+        }
+      RowSums t = rs[r][0];
+#pragma unroll
       for (int off = kLanesPerRow / 2; off > 0; off /= 2) {
-        const double od = __shfl_xor(rs[r].d, off, kWave);
-        const double os = __shfl_xor(rs[r].s, off, kWave);
-        rs[r].d = rs[r].d + od;
-        rs[r].s = rs[r].s + os;
+        const double od = __shfl_xor(t.d, off, kWave);
+        const float os = __shfl_xor(t.s, off, kWave);
+        t.d = t.d + od;
+        t.s = t.s + os;
       }
       const int64_t row = (wave * kSlots + slot) * R + r;
       if (chain0 == 0 && live[r])
-        reinterpret_cast<double2*>(it.sums)[row] = make_double2(rs[r].d, rs[r].s);
+        reinterpret_cast<double2*>(it.sums)[row] = make_double2(t.d, static_cast<double>(t.s));
     }
   }
 
@@ -335,10 +340,10 @@ __global__ void __launch_bounds__(kGroupThreads) gemv_tree_kernel(const GemvBatc
 
 // A GEMV launch that also checks outputs of earlier launches: the first workgroups of the grid
 // each run one (check, block) pair of `ride` (the standalone checker's code, so rho, tau and the
-// verdicts are bit-identical to pck_blocked_check), the rest compute the GEMV rows.  The checked
-// y were written by launches that finished before this one started (stream order), and the
-// checker workgroups are separate wavefronts that read them from memory; their latency hides
-// behind the GEMV's streaming, and the bank reads add about 2.3% (BF16, b = 128) to the bytes.
+// verdicts are bit-identical to pck_blocked_check), the rest compute the GEMV rows.  The checked y were written by launches that finished before this one
+// started (stream order), and the checker workgroups are separate wavefronts that read them from
+// memory; their latency hides behind the GEMV's streaming, and the bank reads add about 2.3%
+// (BF16, b = 128) to the bytes.
 template <int T, int R, int U, bool kFp8, bool kPad, bool kNt>
 __global__ void __launch_bounds__(kGroupThreads)
     gemv_ride_kernel(const GemvBatch batch, const PckCheckBatch ride) {
@@ -351,7 +356,7 @@ __global__ void __launch_bounds__(kGroupThreads)
   gemv_rows<T, R, U, kFp8, true, kPad, kNt>(batch, static_cast<int64_t>(blockIdx.x) - items);
 }
 
-// The in-pass GEMV: the tree's outputs plus each row's FP64 sums (d_i, s_i), and in the first
+// The in-pass GEMV: the tree's outputs plus each row's sums (d_i, s_i), and in the first
 // workgroups of the grid the row-sum checks of `ride` (outputs of earlier launches on the stream,
 // read from memory; one wave per (check, block) pair, the code of pck_rowsum_check, so the
 // results are bit-identical to it).  A check never reads anything this launch writes.
@@ -611,6 +616,7 @@ hipError_t launch_group_rowsums(const PckGemv* gemvs, double* const* sums, int c
   GemvBatch& b = plan.batch;
   const TreeShape shape = choose_rowsum_shape(plan.max_per_lane, plan.rows, kFp8);
   const bool v = plan.vector, p = plan.pad;
+
   switch (threads) {
     case 32: return launch_for_threads<32, kFp8, true>(b, v, p, shape, stream, rs);
     case 64: return launch_for_threads<64, kFp8, true>(b, v, p, shape, stream, rs);

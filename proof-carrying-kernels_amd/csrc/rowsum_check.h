@@ -10,15 +10,18 @@
 //   tau = coef s + geps ((1 + u32) s + sum |y_i|) + tau_floor, every operation rounded up
 // and the block passes only if every y_i is finite, tau is finite and |rho| <= tau.
 //
-// Why the threshold is sound.  d_i is the RN FP64 sum of exact products, of depth D (a lane's
-// (T / min(T, 64)) ceil(ceil(n / V) / T) V sequential terms plus the butterfly's levels), so
-// |d_i - (W x)_i| <= gamma_D(u64) S_i with S_i = sum_j |W_ij x_j|; s_i is the same sum of
-// |products|, so S_i <= s_i / (1 - gamma_D) <= s_i s_factor.  The evaluation of rho adds
-// ceil(b / 64) + 7 levels, so rho's error is within gamma_H(u64) (sum S_i + sum |y_i|) for
-// H >= D + ceil(b / 64) + 7, which geps covers; coef s covers the GEMV tree's own error exactly
-// as in the bank checker (T2/T3), and s here is the exact sum of |W_ij x_j| (bounded above),
-// never more than the bank's a . |x|.
-//
+// Why the threshold is sound.  The products p_j are exact in FP32 (barring underflow, at most
+// 2^-150 each, which tau_floor's 2 b n 2^-150 term covers for d and s).  d_i adds them in pairs
+// in FP32, each pair within u32 (|p0| + |p1|), so sum_i |r_i (d_i - (W x)_i)| <= u32 S + (FP64
+// error) with S = sum_{i, j} |W_ij x_j|: the same u32 S that coef = gamma_h + u32 reserves in
+// the bank checker for c's FP32 rounding.  s_i is the FP32 RN sum of |p_j| of depth D (a lane's
+// (T / min(T, 64)) ceil(ceil(n / V) / T) V terms plus the butterfly's levels), so
+// S_i <= s_i / (1 - gamma_D(u32)) <= s_i s_factor.  The FP64 sums (d's pair sums, the check's
+// per-lane sums and butterfly, the final subtraction) are within gamma_H(u64) (S + sum |y|) for
+// H >= D + ceil(b / 64) + 7, which geps covers.  gamma_h s covers the GEMV tree's own error as
+// in the bank checker (T2/T3); s here bounds the exact S, where the bank's a . |x| carries the
+// BF16 rounding of a on top.
+
 // Order (fixed, so results do not depend on scheduling): lane l of the wave adds rows
 // l, l + 64, l + 128, ... in increasing order into cx, r.y (round to nearest) and s, sum |y|
 // (round up, error-free), then the lanes combine by an xor butterfly over offsets 32, 16, ..., 1

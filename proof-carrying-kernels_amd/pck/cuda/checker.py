@@ -347,7 +347,8 @@ def rowsum_depth(n: int) -> int:
     """Depth D of the in-pass row sums of a row of n columns, for every launch: the most
     additions any term passes through, over thread counts 32..1024 and vectors of 8 or 16
     columns.  Lane l of min(T, 64) lanes adds (T / min(T, 64)) ceil(ceil(n / V) / T) V terms in
-    sequence (padding included: adding +0 is exact), then log2 min(T, 64) butterfly levels."""
+    sequence (padding included: adding +0 is exact; d takes them in pairs, half as many), then
+    log2 min(T, 64) butterfly levels."""
     depth = 0
     for threads in (32, 64, 128, 256, 512, 1024):
         lanes = min(threads, 64)
@@ -360,21 +361,22 @@ def rowsum_depth(n: int) -> int:
 class RowSumChecker:
     """Blocked checks of y = W x from the row sums of an in-pass GEMV launch, with no bank.
 
-    The in-pass launch (`pck.cuda.gemv_group_rowsums`) writes, beside y, the FP64 pair
-    (d_i, s_i) = (sum_j W_ij x_j, sum_j |W_ij x_j|) of every row from the weights it streams,
-    so the check reads 16 bytes per row instead of the bank's 6n bytes per block (2.3% of BF16
-    and 4.7% of FP8 weight bytes at b = 128).  Each (check, block) pair is then the blocked
-    checker's relation (reference `src/pck/cuda/csrc/checker_kernel.cu:115-183`):
-    rho = r . d_beta - r . y_beta and tau = coef s + geps ((1 + u32) s + sum |y|) + tau_floor,
-    with s the exact sum of |W_ij x_j| over the block bounded above.  That s never exceeds the
-    bank's a . |x|, so this threshold is never looser than `GpuBlockedChecker`'s, and it is
-    sound for the same reason (T2/T3: the honest tree error is within coef s; rho's own FP64
-    error within geps).  Signs come from the same draw as `GpuBlockedChecker` (the same
-    generator state gives the same r), ``coef`` and ``tau_floor`` are its values; ``s_factor``
-    = 1 + (D + 1) 2^-52 >= 1 / (1 - D u64) bounds the RN row sums of depth D = `rowsum_depth`
-    (n), and ``geps`` = gamma_H(u64) covers rho's FP64 evaluation, H = D + ceil(b / 64) + 7
-    (the row sums, the check's per-lane sums and butterfly, the final subtraction).  H is far
-    below the bank checker's n + b + 1, so this tau is never above `GpuBlockedChecker`'s.
+    The in-pass launch (`pck.cuda.gemv_group_rowsums`) writes, beside y, a pair per row from
+    the FP32 products p_j = W_ij x_j the tree forms anyway: d_i (consecutive products added in
+    pairs in FP32, the pair sums added in FP64) and s_i (sum of |p_j| in FP32).  The check
+    then reads 16 bytes per row instead of the bank's 6n bytes per block (2.3% of BF16 and 4.7%
+    of FP8 weight bytes at b = 128).  Each (check, block) pair is the blocked checker's
+    relation (reference `src/pck/cuda/csrc/checker_kernel.cu:115-183`): rho = r . d_beta -
+    r . y_beta, tau = coef s + geps ((1 + u32) s + sum |y|) + tau_floor, with s an upper bound
+    of the exact S = sum |W_ij x_j| over the block.  Soundness (T2/T3): coef = gamma_h + u32 as
+    in `GpuBlockedChecker`; gamma_h S covers the GEMV tree's error and u32 S the FP32 pair sums
+    of d (at most u32 (|p0| + |p1|) each), as it covers the FP32 rounding of c there;
+    ``s_factor`` = 1 + (D + 1) 2^-23 bounds the FP32 sums of |p| of depth D = `rowsum_depth`(n);
+    ``geps`` = gamma_H(u64), H = D + ceil(b / 64) + 7, covers rho's FP64 evaluation; and
+    ``tau_floor`` adds 2 b n 2^-150 for FP32 product underflow to the bank checker's n 2^-148.
+    The resulting tau is within (1 + 2^-14) of the threshold for the exact S, where the bank's
+    BF16 column sums a make it up to 2^-8 looser.  Signs come from the same draw as
+    `GpuBlockedChecker` (the same generator state gives the same r).
 
     The check runs inside the producing GEMV's launch sequence: it suits the production
     (non-adversarial) fault model, as the bank checker with signs drawn at weight load does
@@ -405,8 +407,8 @@ class RowSumChecker:
         depth = rowsum_depth(n)
         self.coef = next_up(gamma(height) + U32, 2)
         self.geps = next_up(gamma(depth + ceil_div(block, 64) + 7, U64), 2)
-        self.tau_floor = next_up(n * 2.0**-148, 2)
-        self.s_factor = next_up(1.0 + (depth + 1) * 2.0**-52, 2)
+        self.tau_floor = next_up(n * 2.0**-148 + 2 * block * n * 2.0**-150, 2)
+        self.s_factor = next_up(1.0 + (depth + 1) * 2.0**-23, 2)
 
     @property
     def device(self) -> torch.device:

@@ -8,7 +8,8 @@
 - its verdicts equal the bank checker's (GpuBlockedChecker, same signs) on honest outputs and
   on the planted faults of the reference's campaign (dropped tail, BF16 accumulator, partials
   and output, exponent and sign flips), except where |rho| falls between the two thresholds;
-  its tau is never above the bank checker's;
+  its tau is never more than 2^-14 above the bank checker's (the bank's BF16 column sums are
+  up to 2^-8 above the exact ones);
 - non-finite outputs and weights fail closed; bad arguments raise.
 """
 
@@ -176,15 +177,15 @@ def test_verdicts_equal_bank_checker(fp8: bool, m: int, n: int) -> None:
         b = rs.check(sums[0], yt)
         tau_bank, tau_rs = a.tau.cpu().numpy(), b.tau.cpu().numpy()
         finite = np.isfinite(tau_bank) & np.isfinite(tau_rs)
-        assert (tau_rs[finite] <= tau_bank[finite]).all(), name
+        # the bank's a is BF16 rounded up (up to 2^-8 over the exact column sums), the row sums'
+        # s at most 2^-14 over the exact S
+        assert (tau_rs[finite] <= tau_bank[finite] * (1 + 2.0**-14)).all(), name
         assert np.array_equal(np.isfinite(tau_bank), np.isfinite(tau_rs)), name
         rho = np.abs(a.rho.cpu().numpy())
         clear = (rho < 0.99 * tau_rs) | (rho > 1.01 * tau_bank)
         va, vb = a.passed.cpu().numpy(), b.passed.cpu().numpy()
         assert np.array_equal(va[clear], vb[clear]), name
         in_window += int((~clear).sum())
-        # where they may differ, the row-sum check is the stricter one
-        assert not (vb & ~va).any(), name
         if name == "honest":
             assert va.all() and vb.all()
         elif name in ("exp_flip", "sign_flip", "drop_tail", "bf16_accumulator"):
