@@ -275,6 +275,46 @@ int pck_check_members(const float* logits, int64_t rows, int64_t vocab, const in
                       double slack, int64_t k_lim, int all_k, uint8_t* ok, int64_t* above,
                       double* mass_above, void* stream);
 
+/* The same check with the options a sampler hook needs in one launch (the reference's plugin
+ * builds these with torch ops around its check, src/pck/vllm_plugin.py:146-186):
+ *   top_p            FP64, or FP32 when top_p_fp32 = 1 (widened exactly), or NULL;
+ *   temperature      (requests,) FP32 with temperature_index (rows,) int64: row r is greedy
+ *                    iff temperature[temperature_index[r]] == 0 (vLLM's per-request sampling
+ *                    state); NULL: greedy as in pck_check_members;
+ *   injected         (rows,) uint8 faults the caller planted, or NULL;
+ *   ok, above, mass_above   outputs as in pck_check_members; each may be NULL;
+ *   totals           NULL, or 6 words the kernel adds each row into (64-bit atomics):
+ *                    [0] rows, [1] rejected, [2] injected, [3] rejected and injected,
+ *                    [4] rejected and not injected, [5] maximum of K(r - p) over accepted,
+ *                    non-greedy rows with p < 1, where K is the order-preserving key of an FP64
+ *                    value v: bits(v) | 2^63 for v >= 0, ~bits(v) for v < 0.  The caller
+ *                    initialises the buffer (word 5 to K(-1) for "none yet") and may keep
+ *                    adding to it across calls.
+ * No reference counterpart as a native entry; pck_check_members is this with every option
+ * off. */
+typedef struct PckMemberArgs {
+  const float* logits;
+  int64_t rows;
+  int64_t vocab;
+  const int64_t* tokens;
+  const int64_t* top_k;
+  const void* top_p;
+  const uint8_t* greedy;
+  const float* temperature;
+  const int64_t* temperature_index;
+  const uint8_t* injected;
+  double slack;
+  int64_t k_lim;
+  int32_t all_k;
+  int32_t top_p_fp32;
+  uint8_t* ok;
+  int64_t* above;
+  double* mass_above;
+  unsigned long long* totals;
+} PckMemberArgs;
+
+int pck_check_members_ex(const PckMemberArgs* args, void* stream);
+
 /* ---------------------------------------------------------------------------------------------
  * Set-sampling checker (top-k / top-p): is sel[b, 0 .. len[b]) a valid top-k set (top_p = 0,
  * length k) or a valid minimal top-p nucleus (top_p = 1) of row b of logits (rows, vocab) FP32?

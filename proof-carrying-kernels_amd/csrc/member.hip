@@ -47,21 +47,14 @@ constexpr int kWaves = kThreads / kWave;
 constexpr int kCap = 4096;  // candidates held in LDS
 constexpr int64_t kPrefix = 16 * kThreads;  // logits that set the candidate threshold
 
-struct MemberArgs {
-  const float* logits;
-  int64_t rows;
-  int64_t vocab;
-  const int64_t* tokens;
-  const int64_t* top_k;
-  const double* top_p;
-  const uint8_t* greedy;
-  double slack;
-  int64_t k_lim;
-  int all_k;
-  uint8_t* ok;
-  int64_t* above;
-  double* mass_above;
-};
+using MemberArgs = PckMemberArgs;
+
+// Order-preserving 64-bit key of an FP64 value (a larger value has a larger key), for the
+// totals' running maximum of r - p, kept with an unsigned atomic maximum.
+__device__ __forceinline__ unsigned long long order_key64(double v) {
+  const unsigned long long u = static_cast<unsigned long long>(__double_as_longlong(v));
+  return (u >> 63) ? ~u : (u | 0x8000000000000000ull);
+}
 
 // Order-preserving key: a larger float has a larger key; -0 and +0 share the key of +0.
 __device__ __forceinline__ uint32_t order_key(float f) {
@@ -314,10 +307,16 @@ __global__ void __launch_bounds__(kThreads) member_kernel(const MemberArgs A) {
   // a requested top-k is clamped to [1, vocab] (reference src/pck/member.py:153)
   const int64_t k_req = A.top_k ? A.top_k[r] : vocab;
   const int64_t k_row = k_req < 1 ? 1 : (k_req > vocab ? vocab : k_req);
-  const bool greedy = A.greedy ? A.greedy[r] != 0 : false;
-  const double p = A.top_p ? A.top_p[r] : 1.0;
+  // Greedy rows: the caller's flags, or temperature 0 of the row's request (vLLM's sampling
+  // state, read through the row's request index).
+  const bool greedy = A.temperature ? A.temperature[A.temperature_index[r]] == 0.0f
+                                    : (A.greedy ? A.greedy[r] != 0 : false);
+  const bool has_p = A.top_p != nullptr;
+  const double p = !has_p ? 1.0
+                   : A.top_p_fp32 ? static_cast<double>(static_cast<const float*>(A.top_p)[r])
+                                  : static_cast<const double*>(A.top_p)[r];
 
-  const bool want_mass = A.top_p != nullptr && p < 1.0;
+  const bool want_mass = has_p && p < 1.0;
   const bool use_kth = A.all_k || (A.k_lim > 0 && k_row < vocab);
   const int64_t k_eff = k_row < A.k_lim ? k_row : A.k_lim;
   const bool fused = want_mass && use_kth && k_eff <= kThreads;
@@ -447,28 +446,61 @@ __global__ void __launch_bounds__(kThreads) member_kernel(const MemberArgs A) {
     ok = ok && (greedy || ratio < high);
   }
   if (t == 0) {
-    A.ok[r] = ok;
-    A.above[r] = above;
-    A.mass_above[r] = mass;
+    if (A.ok) A.ok[r] = ok;
+    if (A.above) A.above[r] = above;
+    if (A.mass_above) A.mass_above[r] = mass;
+    if (A.totals) {
+      // Running totals (integer atomics, so the sums do not depend on the order of rows):
+      // rows, rejected, injected, caught (rejected and injected), false alarms (rejected, not
+      // injected), and the maximum of r - p over accepted top-p rows not greedy (the key of
+      // -1 is the host's initial value: no such row yet).
+      unsigned long long* tot = A.totals;
+      const bool injected = A.injected ? A.injected[r] != 0 : false;
+      atomicAdd(&tot[0], 1ull);
+      if (!ok) atomicAdd(&tot[1], 1ull);
+      if (injected) atomicAdd(&tot[2], 1ull);
+      if (!ok && injected) atomicAdd(&tot[3], 1ull);
+      if (!ok && !injected) atomicAdd(&tot[4], 1ull);
+      if (ok && want_mass && !greedy) atomicMax(&tot[5], order_key64(mass - p));
+    }
   }
 }
 
 }  // namespace
 }  // namespace pck
 
+extern "C" int pck_check_members_ex(const PckMemberArgs* args, void* stream) {
+  if (args == nullptr) return hipErrorInvalidValue;
+  const PckMemberArgs& a = *args;
+  if (a.rows < 0 || a.rows * pck::kThreads > 0xFFFFFFFFll || a.vocab < 1 ||
+      a.vocab > 0x7FFFFFFF || a.k_lim < 0 || a.k_lim > a.vocab)
+    return hipErrorInvalidValue;
+  if (a.rows == 0) return hipSuccess;
+  if (!a.logits || !a.tokens || (a.temperature && !a.temperature_index)) return hipErrorInvalidValue;
+  if (a.all_k && a.k_lim < 1) return hipErrorInvalidValue;
+  pck::member_kernel<<<dim3(static_cast<unsigned>(a.rows)), dim3(pck::kThreads), 0,
+                       static_cast<hipStream_t>(stream)>>>(a);
+  return hipGetLastError();
+}
+
 extern "C" int pck_check_members(const float* logits, int64_t rows, int64_t vocab,
                                  const int64_t* tokens, const int64_t* top_k, const double* top_p,
                                  const uint8_t* greedy, double slack, int64_t k_lim, int all_k,
                                  uint8_t* ok, int64_t* above, double* mass_above, void* stream) {
-  if (rows < 0 || rows * pck::kThreads > 0xFFFFFFFFll || vocab < 1 || vocab > 0x7FFFFFFF ||
-      k_lim < 0 || k_lim > vocab)
-    return hipErrorInvalidValue;
-  if (rows == 0) return hipSuccess;
-  if (!logits || !tokens || !ok || !above || !mass_above) return hipErrorInvalidValue;
-  if (all_k && k_lim < 1) return hipErrorInvalidValue;
-  const pck::MemberArgs args{logits, rows,  vocab, tokens, top_k, top_p, greedy,
-                             slack,  k_lim, all_k, ok,     above, mass_above};
-  pck::member_kernel<<<dim3(static_cast<unsigned>(rows)), dim3(pck::kThreads), 0,
-                       static_cast<hipStream_t>(stream)>>>(args);
-  return hipGetLastError();
+  if (rows > 0 && (!ok || !above || !mass_above)) return hipErrorInvalidValue;
+  PckMemberArgs a{};
+  a.logits = logits;
+  a.rows = rows;
+  a.vocab = vocab;
+  a.tokens = tokens;
+  a.top_k = top_k;
+  a.top_p = top_p;
+  a.greedy = greedy;
+  a.slack = slack;
+  a.k_lim = k_lim;
+  a.all_k = all_k;
+  a.ok = ok;
+  a.above = above;
+  a.mass_above = mass_above;
+  return pck_check_members_ex(&a, stream);
 }

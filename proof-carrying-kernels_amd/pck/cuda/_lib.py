@@ -112,6 +112,29 @@ class PckRowSumBatch(ctypes.Structure):
     ]
 
 
+class PckMemberArgs(ctypes.Structure):
+    _fields_ = [
+        ("logits", _p),
+        ("rows", _i64),
+        ("vocab", _i64),
+        ("tokens", _p),
+        ("top_k", _p),
+        ("top_p", _p),
+        ("greedy", _p),
+        ("temperature", _p),
+        ("temperature_index", _p),
+        ("injected", _p),
+        ("slack", _f64),
+        ("k_lim", _i64),
+        ("all_k", _i32),
+        ("top_p_fp32", _i32),
+        ("ok", _p),
+        ("above", _p),
+        ("mass_above", _p),
+        ("totals", _p),
+    ]
+
+
 # name -> (argtypes); every entry point returns int (a hipError_t value)
 SIGNATURES: dict[str, list[Any]] = {
     "pck_gemv_bf16_naive": [_p, _p, _p, _i64, _i64, _int, _p],
@@ -135,6 +158,7 @@ SIGNATURES: dict[str, list[Any]] = {
     "pck_check_members": [
         _p, _i64, _i64, _p, _p, _p, _p, _f64, _i64, _int, _p, _p, _p, _p,
     ],  # fmt: skip
+    "pck_check_members_ex": [ctypes.POINTER(PckMemberArgs), _p],
     "pck_sampling_check": [
         _p, _p, _p, _i64, _i64, _i64, _i64, _int, _f64, _f64, _f64, _i64,
         _p, _p, _p, _p, _p, _p, _p, _p,

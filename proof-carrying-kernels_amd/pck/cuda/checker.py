@@ -490,17 +490,33 @@ def check_batched(
     direct = [item for item in items if _batched_kernel_fits(*item)]
     out: dict[int, CheckResult] = {}
     for item in items:
-        if not _batched_kernel_fits(*item):  # one single-vector check per column
-            ch, X, Y = item
-            cols = check_many([(ch, X[b].contiguous(), Y[b].contiguous()) for b in range(X.size(0))])
-            out[id(item)] = CheckResult(
-                torch.stack([r.passed for r in cols], dim=-1),
-                torch.stack([r.rho for r in cols], dim=-1),
-                torch.stack([r.tau for r in cols], dim=-1),
-            )
+        if not _batched_kernel_fits(*item):
+            out[id(item)] = _check_columns(*item)
     for res, item in zip(_check_batched_direct(direct), direct):
         out[id(item)] = res
     return [out[id(item)] for item in items]
+
+
+def _check_columns(ch: GpuBlockedChecker, X: torch.Tensor, Y: torch.Tensor) -> CheckResult:
+    """Every column of Y checked as one GEMV output, up to eight columns per launch of the
+    single-vector kernel, all against the same bank (this kernel uses no scratch, so one
+    checker may fill several descriptors of a launch); results (checks, num_blocks, B)."""
+    if not (X.dim() == 2 and Y.dim() == 2 and X.size(0) == Y.size(0)):
+        raise RuntimeError("X must be (B, n) and Y (B, m) with the same B")
+    cols = []
+    for b0 in range(0, X.size(0), MAX_BATCH):
+        xs = [X[b].contiguous() for b in range(b0, min(b0 + MAX_BATCH, X.size(0)))]
+        ys = [Y[b].contiguous() for b in range(b0, min(b0 + MAX_BATCH, X.size(0)))]
+        k = len(xs)
+        batch, outputs, device = build_batch(
+            [ch.c] * k, [ch.a] * k, [ch.r] * k, xs, ys, [ch._partial_cx] * k, [ch._partial_s] * k,
+            [ch._counters] * k, [ch.coef] * k, [ch.geps] * k, [ch.tau_floor] * k,
+        )  # fmt: skip
+        with torch.cuda.device(device):
+            err = lib().pck_blocked_check(batch, stream_handle(device))
+        check(err, "checker kernel launch")
+        cols.extend(outputs)
+    return CheckResult(*(torch.stack([c[i] for c in cols], dim=-1) for i in range(3)))
 
 
 def _batched_kernel_fits(ch: GpuBlockedChecker, X: torch.Tensor, Y: torch.Tensor) -> bool:
@@ -557,41 +573,57 @@ def _check_batched_direct(
 
 
 class PendingCheck:
-    """A check queued on a side stream; `wait` makes the current stream wait for it
-    (reference `src/pck/cuda/checker.py:174-186`)."""
+    """A check running on a `SideStreamChecker`'s stream (reference name and use,
+    `src/pck/cuda/checker.py:174-186`).  Its result tensors were allocated on the submitting
+    stream, so `wait` there only orders that stream after the check's completion event."""
 
-    def __init__(self, result: CheckResult, done: torch.cuda.Event) -> None:
+    def __init__(self, result: CheckResult, done: torch.cuda.Event, owner: torch.cuda.Stream) -> None:
         self._result = result
         self._done = done
+        self._owner = owner
 
     def wait(self) -> CheckResult:
-        stream = torch.cuda.current_stream()
-        stream.wait_event(self._done)
-        for t in (self._result.passed, self._result.rho, self._result.tau):
-            t.record_stream(stream)
+        """Make the current stream wait for the check and return its result."""
+        current = torch.cuda.current_stream(self._owner.device)
+        current.wait_event(self._done)
+        if current != self._owner:  # keep the allocator from recycling them under this stream
+            for t in (self._result.passed, self._result.rho, self._result.tau):
+                t.record_stream(current)
         return self._result
+
+    def done(self) -> bool:
+        """Whether the check has finished (never waits)."""
+        return bool(self._done.query())
 
 
 class SideStreamChecker:
-    """Runs checks on a dedicated stream (default priority) so they overlap later work; each
-    check waits for an event recorded on the caller's stream at submit time, so it starts only
-    after the GEMV that produced y (reference `src/pck/cuda/checker.py:189-215`)."""
+    """Runs blocked checks on a stream of its own (default priority), so a check overlaps the
+    work the caller enqueues after it (reference name and use, `src/pck/cuda/checker.py:189-215`).
+
+    `submit` validates and allocates on the caller's current stream, records an event there (so
+    the check starts only after the kernel that produced y), and launches on the side stream;
+    inputs and outputs are marked as used by the side stream for the allocator.  Checks on one
+    side stream run in submission order, so a checker's state is never used by two at once.
+    """
 
     def __init__(self, device: torch.device | None = None) -> None:
         self.stream = torch.cuda.Stream(device)
 
     def submit(self, checker: GpuBlockedChecker, x: torch.Tensor, y: torch.Tensor) -> PendingCheck:
-        ready = torch.cuda.Event()
-        ready.record(torch.cuda.current_stream())
-        with torch.cuda.stream(self.stream):
-            self.stream.wait_event(ready)
-            x.record_stream(self.stream)  # keep the allocator from reusing x and y early
-            y.record_stream(self.stream)
-            result = checker.check(x, y)
-            done = torch.cuda.Event()
-            done.record(self.stream)
-        return PendingCheck(result, done)
+        caller = torch.cuda.current_stream(self.stream.device)
+        batch, (result,), device = batch_for([(checker, x, y)])
+        produced = torch.cuda.Event()
+        produced.record(caller)
+        self.stream.wait_event(produced)
+        for t in (x, y, result.passed, result.rho, result.tau):
+            t.record_stream(self.stream)
+        with torch.cuda.device(device):
+            err = lib().pck_blocked_check(batch, int(self.stream.cuda_stream))
+        check(err, "checker kernel launch")
+        done = torch.cuda.Event()
+        done.record(self.stream)
+        return PendingCheck(result, done, caller)
 
     def wait_all(self) -> None:
         """Make the current stream wait for every check submitted so far."""
-        torch.cuda.current_stream().wait_stream(self.stream)
+        torch.cuda.current_stream(self.stream.device).wait_stream(self.stream)

@@ -148,37 +148,48 @@ def check_topp_gpu(
 def topk_sample(
     logits: torch.Tensor, k: int, generator: torch.Generator | None = None
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """Untrusted sampler: torch.topk, then a draw within the set.  Returns (selected, token)
-    (reference `cuda/sampling.py:96-103`)."""
+    """Untrusted top-k sampler for the checker to judge (the role of the reference's
+    `cuda/sampling.py:96-103`): the k largest logits per row, then one token drawn from their
+    softmax by the Gumbel-max trick (argmax of value + Gumbel noise).  Returns (selected (B, k),
+    token (B,))."""
     values, idx = torch.topk(logits, k, dim=-1)
-    pick = torch.multinomial(torch.softmax(values, dim=-1), 1, generator=generator)
+    u = torch.rand(values.shape, generator=generator, device=logits.device, dtype=torch.float64)
+    gumbel = -torch.log(-torch.log(u.clamp_min(1e-300)))
+    pick = (values.double() + gumbel).argmax(dim=-1, keepdim=True)
     return idx, idx.gather(-1, pick).squeeze(-1)
 
 
 def topp_select(
     logits: torch.Tensor, p: float, temperature: float = 1.0
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """Untrusted top-p (reference `cuda/sampling.py:106-121`): FP32 softmax, a stable
-    descending sort, an FP64 running mass, and the shortest prefix reaching p.  Returns
-    (selected (B, V) sorted indices, lengths (B,)); the first lengths[b] entries of row b are
-    the nucleus."""
-    probs = torch.softmax(logits / temperature, dim=-1)
-    sorted_probs, order = torch.sort(probs, dim=-1, descending=True, stable=True)
-    running = torch.cumsum(sorted_probs.double(), dim=-1)
-    lengths = (running < p).sum(dim=-1) + 1
+    """Untrusted top-p selection for the checker to judge (the role of the reference's
+    `cuda/sampling.py:106-121`): logits sorted in descending order (stable, so ties keep
+    index order), their probabilities exp((l - max) / T) normalised in FP64, and the shortest
+    prefix whose cumulative mass reaches p (searchsorted).  Returns (selected (B, V) indices in
+    that order, lengths (B,)); the first lengths[b] entries of row b are the nucleus."""
+    scaled = logits.double() / temperature
+    ordered, order = torch.sort(scaled, dim=-1, descending=True, stable=True)
+    weights = torch.exp(ordered - ordered[:, :1])
+    cumulative = torch.cumsum(weights, dim=-1)
+    target = (p * cumulative[:, -1:]).contiguous()
+    lengths = torch.searchsorted(cumulative.contiguous(), target, right=False).squeeze(-1) + 1
     return order.contiguous(), lengths.clamp(max=logits.shape[1]).to(torch.int64)
 
 
 def sharded_topk_gpu(logits: torch.Tensor, k: int, shards: int, per_shard: int) -> torch.Tensor:
-    """Untrusted approximate top-k: the ``per_shard`` largest of each of ``shards`` equal
-    shards, then the k largest of those (the fault model of `pck.faults.sharded_topk`;
-    reference `cuda/sampling.py:124-136`)."""
+    """Untrusted approximate top-k (the fault model of `pck.faults.sharded_topk`; the role of
+    the reference's `cuda/sampling.py:124-136`): a logit is a candidate if it ranks among the
+    ``per_shard`` largest of its shard (equal shards, ties to the lower index); the result is
+    the k largest candidates, ties to the lower index.  Exact when per_shard >= k."""
     rows, vocab = logits.shape
     if vocab % shards or per_shard > vocab // shards or k > shards * per_shard:
         raise ValueError("need vocab % shards == 0, per_shard <= vocab / shards, k <= pool")
     width = vocab // shards
-    _, local = torch.topk(logits.view(rows, shards, width), per_shard, dim=-1)
-    offsets = torch.arange(shards, device=logits.device).view(1, shards, 1) * width
-    pool = (local + offsets).view(rows, -1)
-    _, pick = torch.topk(logits.gather(-1, pool), k, dim=-1)
-    return pool.gather(-1, pick)
+    by_shard = logits.reshape(rows, shards, width)
+    order = torch.sort(by_shard, dim=-1, descending=True, stable=True).indices
+    rank = torch.empty_like(order).scatter_(
+        -1, order, torch.arange(width, device=logits.device).expand_as(order)
+    )
+    candidate = (rank < per_shard).reshape(rows, vocab)
+    masked = torch.where(candidate, logits, torch.full_like(logits, -float("inf")))
+    return torch.sort(masked, dim=-1, descending=True, stable=True).indices[:, :k].contiguous()

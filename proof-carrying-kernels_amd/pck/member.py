@@ -51,6 +51,133 @@ def _host_top_k(top_k: Any, top_k_host: Any, vocab: int) -> tuple[int, bool]:
     return (int(lim.max()), lim.size == hk.size) if lim.size else (0, False)
 
 
+EXCESS_NONE = -1.0
+"""max_excess before any accepted top-p row (r - p >= -1 always)."""
+
+
+def excess_key(v: float) -> int:
+    """The order-preserving 64-bit key the membership kernel keeps the running maximum of
+    r - p in (a larger value has a larger key)."""
+    u = int(np.array([v], dtype=np.float64).view(np.uint64)[0])
+    return (~u & (2**64 - 1)) if u >> 63 else u | (1 << 63)
+
+
+def excess_value(key: int) -> float:
+    """Inverse of `excess_key`."""
+    u = (key & ~(1 << 63)) if key >> 63 else (~key & (2**64 - 1))
+    return float(np.array([u], dtype=np.uint64).view(np.float64)[0])
+
+
+def key_as_int64(key: int) -> int:
+    """The signed 64-bit integer with the same bits as the unsigned ``key``."""
+    return key - 2**64 if key >= 2**63 else key
+
+
+def new_totals(device: Any) -> Any:
+    """A device buffer for `launch_check` to add a batch's counts into: rows, rejected,
+    injected, caught, false alarms, and the key of the largest r - p so far (none yet)."""
+    import torch
+
+    host = torch.zeros(6, dtype=torch.int64)
+    host[5] = key_as_int64(excess_key(EXCESS_NONE))
+    return host.to(device)
+
+
+def launch_check(
+    logits: Any,
+    tokens: Any,
+    top_k: Any = None,
+    top_p: Any = None,
+    greedy: Any = None,
+    tol: float = 1e-4,
+    top_k_host: Any = None,
+    *,
+    temperature: Any = None,
+    temperature_index: Any = None,
+    injected: Any = None,
+    totals: Any = None,
+    outputs: bool = True,
+) -> dict[str, Any] | None:
+    """One launch of the membership kernel (`pck_check_members_ex`) over a batch.
+
+    Beside `check_members`'s arguments: ``temperature`` (requests,) FP32 with
+    ``temperature_index`` (B,) makes row r greedy iff temperature[index[r]] == 0 (instead of
+    ``greedy``); ``top_p`` may be FP32 (read as is) or FP64; ``injected`` (B,) bool marks planted
+    faults; ``totals`` (from `new_totals`) receives the batch's counts on the device.  Returns
+    the outputs (``ok``, ``above``, ``mass_above``) unless ``outputs`` is False.  Never
+    synchronises: top-k's host copy is ``top_k_host`` (or one copy of ``top_k``)."""
+    import torch
+
+    from pck.cuda._lib import PckMemberArgs, check, lib, stream_handle
+
+    if not logits.is_cuda:
+        raise RuntimeError(
+            "check_members runs the HIP membership kernel and needs logits on the GPU, "
+            f"got {logits.device}"
+        )
+    device = logits.device
+    lv = logits.float().contiguous()
+    if lv.dim() != 2:
+        raise RuntimeError(f"expected logits of shape (B, V), got {list(lv.shape)}")
+    rows, vocab = lv.shape
+    keep = [lv]
+
+    def dev(x: Any, dtype: Any, name: str) -> int | None:
+        if x is None:
+            return None
+        t = x.to(device=device, dtype=dtype).reshape(rows).contiguous() if dtype else x
+        if t.numel() != rows:
+            raise RuntimeError(f"{name} must have {rows} entries, got {t.numel()}")
+        keep.append(t)
+        return int(t.data_ptr())
+
+    a = PckMemberArgs()
+    a.logits, a.rows, a.vocab = lv.data_ptr(), rows, vocab
+    a.tokens = dev(tokens, torch.long, "tokens")
+    if top_k is not None:  # clamped to [1, V] by the kernel
+        a.top_k = dev(top_k, torch.long, "top_k")
+        a.k_lim, a.all_k = _host_top_k(top_k, top_k_host, vocab)
+    if top_p is not None:
+        fp32 = top_p.dtype == torch.float32
+        a.top_p = dev(top_p, torch.float32 if fp32 else torch.float64, "top_p")
+        a.top_p_fp32 = int(fp32)
+    if temperature is not None:
+        t = temperature.to(device=device, dtype=torch.float32).contiguous()
+        keep.append(t)
+        a.temperature = t.data_ptr()
+        a.temperature_index = dev(temperature_index, torch.long, "temperature_index")
+    elif greedy is not None:  # a bool tensor is read as its bytes (0 or 1)
+        g = greedy.to(device=device, dtype=torch.bool).reshape(rows).contiguous().view(torch.uint8)
+        a.greedy = dev(g, None, "greedy")
+    if injected is not None:
+        inj = injected.to(device=device, dtype=torch.bool).reshape(rows).contiguous().view(torch.uint8)
+        a.injected = dev(inj, None, "injected")
+    if totals is not None:
+        if not (totals.is_cuda and totals.device == device and totals.dtype == torch.int64
+                and totals.numel() == 6 and totals.is_contiguous()):  # fmt: skip
+            raise RuntimeError("totals must be a contiguous (6,) int64 tensor on the logits' device")
+        a.totals = totals.data_ptr()
+    out = None
+    if outputs:
+        # the three outputs in one allocation: [mass_above | above | ok]
+        buf = torch.empty(17 * rows, dtype=torch.uint8, device=device)
+        out = {
+            "ok": buf[16 * rows :].view(torch.bool),
+            "above": buf[8 * rows : 16 * rows].view(torch.int64),
+            "mass_above": buf[: 8 * rows].view(torch.float64),
+        }
+        a.ok, a.above, a.mass_above = (
+            out["ok"].data_ptr(), out["above"].data_ptr(), out["mass_above"].data_ptr()
+        )  # fmt: skip
+    if rows == 0:
+        return out
+    a.slack = next_up(tol + member_eps32(vocab))
+    with torch.cuda.device(device):
+        err = lib().pck_check_members_ex(a, stream_handle(device))
+    check(err, "membership check launch")
+    return out
+
+
 def check_members(
     logits: Any,
     tokens: Any,
@@ -69,49 +196,6 @@ def check_members(
     are copied from ``top_k`` once.  Returns device tensors ``ok`` (B,) bool, ``above`` (B,)
     int64 and ``mass_above`` (B,) float64.
     """
-    import torch
-
-    from pck.cuda._lib import check, lib, stream_handle
-
-    if not logits.is_cuda:
-        raise RuntimeError(
-            "check_members runs the HIP membership kernel and needs logits on the GPU, "
-            f"got {logits.device}"
-        )
-    device = logits.device
-    lv = logits.float().contiguous()
-    if lv.dim() != 2:
-        raise RuntimeError(f"expected logits of shape (B, V), got {list(lv.shape)}")
-    rows, vocab = lv.shape
-    t = tokens.reshape(rows).to(device=device, dtype=torch.long).contiguous()
-    k_dev = None
-    k_lim, all_k = 0, False
-    if top_k is not None:  # clamped to [1, V] by the kernel
-        k_dev = top_k.to(device=device, dtype=torch.long).reshape(rows).contiguous()
-        k_lim, all_k = _host_top_k(top_k, top_k_host, vocab)
-    p_dev = None
-    if top_p is not None:
-        p_dev = top_p.to(device=device, dtype=torch.float64).reshape(rows).contiguous()
-    g_dev = None
-    if greedy is not None:  # a bool tensor is read as its bytes (0 or 1)
-        g_dev = greedy.to(device=device, dtype=torch.bool).reshape(rows).contiguous().view(torch.uint8)
-    # the three outputs in one allocation: [mass_above | above | ok]
-    out = torch.empty(17 * rows, dtype=torch.uint8, device=device)
-    mass_above = out[: 8 * rows].view(torch.float64)
-    above = out[8 * rows : 16 * rows].view(torch.int64)
-    ok = out[16 * rows :].view(torch.bool)
-    if rows == 0:
-        return {"ok": ok, "above": above, "mass_above": mass_above}
-    slack = next_up(tol + member_eps32(vocab))
-
-    def ptr(x: Any) -> int | None:
-        return None if x is None else x.data_ptr()
-
-    with torch.cuda.device(device):
-        err = lib().pck_check_members(
-            lv.data_ptr(), rows, vocab, t.data_ptr(), ptr(k_dev), ptr(p_dev), ptr(g_dev), slack,
-            k_lim, int(all_k), ok.data_ptr(), above.data_ptr(), mass_above.data_ptr(),
-            stream_handle(device),
-        )  # fmt: skip
-    check(err, "membership check launch")
-    return {"ok": ok, "above": above, "mass_above": mass_above}
+    out = launch_check(logits, tokens, top_k, top_p, greedy, tol, top_k_host)
+    assert out is not None
+    return out

@@ -119,6 +119,25 @@ def test_batched_equals_the_single_vector_checker() -> None:
             np.testing.assert_array_equal(res.passed[:, :, b].cpu().numpy(), single.passed.cpu().numpy())
 
 
+@pytest.mark.parametrize("n,B", [(1001, 2), (1001, 19), (4100, 9)])
+def test_shapes_off_the_batched_kernel_check_column_by_column(n: int, B: int) -> None:
+    """n % 8 != 0 (the batched kernel's loads need n % 8 == 0): every column goes through the
+    single-vector kernel, eight per launch with the same bank; results equal check_many on each
+    column, faulty columns included."""
+    m = 256
+    _, _, Wt, Xt = problem(m, n, B, seed=n + B)
+    checker = GpuBlockedChecker(Wt, 128, batched_height(n), checks=2, generator=torch.Generator().manual_seed(3))
+    Y = gemm_batched(Wt, Xt)
+    Y[B - 1, 130] += 5.0  # block 1 of the last column
+    res = checker.check_batched(Xt, Y)
+    assert res.passed.shape == (2, m // 128, B)
+    for b in range(B):
+        single = check_many([(checker, Xt[b].contiguous(), Y[b].contiguous())])[0]
+        assert torch.equal(res.passed[:, :, b], single.passed)
+        assert torch.equal(res.rho[:, :, b], single.rho) and torch.equal(res.tau[:, :, b], single.tau)
+    assert res.verdict[:, : B - 1].all() and res.verdict[:, B - 1].tolist() == [True, False]
+
+
 def tau_and_rho_within_bounds(X: NDArray[np.float32], Xt: torch.Tensor, Wt: torch.Tensor, n: int,
                               rel: Fraction) -> None:
     checker = GpuBlockedChecker(Wt, 32, batched_height(n), checks=2, generator=torch.Generator().manual_seed(9))

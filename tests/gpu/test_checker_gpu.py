@@ -18,7 +18,7 @@ from numpy.typing import NDArray
 from oracle.checker import BlockedChecker, gpu_rho_exact, gpu_threshold_exact
 from oracle.gemv import emulate_gemv
 from pck.cuda import GpuBlockedChecker, SideStreamChecker, check_many, gemv_coalesced, gemv_naive
-from pck.cuda._ext import extension
+from pck.cuda.checker import blocked_check
 from pck.fp import U32, bf16, gamma, tree_height
 
 pytestmark = [
@@ -315,18 +315,19 @@ def test_rejects_same_checker_twice() -> None:
         check_many([item, item])
 
 
-def test_extension_rejects_bad_batches() -> None:
+def test_native_entry_rejects_bad_batches() -> None:
+    """The launch entry with the reference's pybind argument lists (bindings.cpp:221-256)."""
     checker, x, y = make_item(*CONFIGS[0], seed=0)
     args = [checker.c, checker.a, checker.r, x, y, checker._partial_cx, checker._partial_s,
             checker._counters, checker.coef, checker.geps, checker.tau_floor]  # fmt: skip
     with pytest.raises(RuntimeError, match="batch size"):
-        extension().blocked_check(*([] for _ in args))
+        blocked_check(*([] for _ in args))
     with pytest.raises(RuntimeError, match="batch size"):
-        extension().blocked_check(*([a] * 9 for a in args))
+        blocked_check(*([a] * 9 for a in args))
     lists = [[a] for a in args]
     lists[4] = [y, y]
     with pytest.raises(RuntimeError, match="same length"):
-        extension().blocked_check(*lists)
+        blocked_check(*lists)
 
 
 # ---- side stream ------------------------------------------------------------------------------

@@ -45,3 +45,20 @@ def test_bad_arguments_are_refused() -> None:
     assert call(src.data_ptr() + 4, 64, sink.data_ptr(), 4, stream) != 0  # misaligned
     assert call(src.data_ptr(), 64, sink.data_ptr(), 0, stream) != 0  # no workgroups
     assert call(ctypes.c_void_p(None), 64, sink.data_ptr(), 4, stream) != 0
+
+
+def test_cold_timer_times_the_function_not_the_flush() -> None:
+    """ColdL2Timer: the flush buffer spans twice L2 plus the MALL; a spin kernel of 2N cycles
+    times about twice one of N (the flush before each rep is outside the timed events); the
+    reported quantiles are ordered; a 1 GiB device copy runs at a plausible rate."""
+    from pck.cuda.timing import ColdL2Timer, cache_bytes, copy_bandwidth_gbps
+
+    timer = ColdL2Timer(warmup=2, reps=12)
+    assert timer.flush.numel() >= 2 * cache_bytes() >= 2 * (256 << 20)
+    short = timer(lambda: torch.cuda._sleep(2_000_000))
+    long = timer(lambda: torch.cuda._sleep(4_000_000))
+    for t in (short, long):
+        assert 0 < t.p10_ms <= t.median_ms <= t.p90_ms
+    assert 1.7 < long.median_ms / short.median_ms < 2.3
+    gbps = copy_bandwidth_gbps(ColdL2Timer(1, 5))
+    assert 500 < gbps < 16_000

@@ -92,7 +92,7 @@ def test_malformed_or_nan_fails_only_its_row(fault: str) -> None:
 
 @pytest.mark.parametrize("vocab", [10, 1000, 151_936])
 @pytest.mark.parametrize(("p", "temp"), [(0.5, 1.0), (0.9, 0.7), (0.95, 1.5), (1.0, 1.0)])
-def test_fp32_topp_sampler_passes_and_masses_are_within_the_slack(vocab: int, p: float, temp: float) -> None:
+def test_topp_sampler_passes_and_masses_are_within_the_slack(vocab: int, p: float, temp: float) -> None:
     print(f"topp vocab={vocab} p={p} temp={temp}", flush=True)
     lg = logits(8, vocab, seed=vocab, scale=2.0)
     selected, lengths = topp_select(lg, p, temp)
@@ -220,15 +220,15 @@ def test_short_and_long_nuclei_in_one_call_match_cpu() -> None:
     assert honest.passed.all()
 
 
-def test_extension_exposes_the_pybind_sampling_check() -> None:
-    """`pck.cuda._ext.extension().sampling_check` takes the reference's pybind arguments
+def test_native_entry_takes_the_pybind_sampling_arguments() -> None:
+    """`pck.cuda.sampling.sampling_check` takes the reference's pybind arguments
     (bindings.cpp:331-334) and returns its five outputs."""
-    from pck.cuda._ext import extension
+    from pck.cuda.sampling import sampling_check
 
     lg = logits(2, 1000, seed=40)
     sel, _ = topk_sample(lg, 10)
     lengths = torch.full((2,), 10, dtype=torch.int64, device="cuda")
-    out = extension().sampling_check(lg, sel, lengths, 10, False, 1.0, 1.0, 0.0, 1)
+    out = sampling_check(lg, sel, lengths, 10, False, 1.0, 1.0, 0.0, 1)
     ref = check_topk_gpu(lg, sel, 10, segments=1)
     assert len(out) == 5 and bool(out[0].all())
     assert torch.equal(out[0], ref.passed) and torch.equal(out[1], ref.min_selected)

@@ -143,18 +143,18 @@ def test_llama_shapes_on_the_default_and_exploit_knobs() -> None:
 
 
 def test_bad_rows_per_block_and_threads_are_rejected() -> None:
-    from pck.cuda._ext import extension
+    from pck.cuda.template import _template
 
     W = torch.zeros(4, 64, dtype=torch.bfloat16, device="cuda")
     x = torch.zeros(64, dtype=torch.bfloat16, device="cuda")
     with pytest.raises(RuntimeError, match="launch failed"):
-        extension().gemv_template(W, x, 64, 4, 8, 1, 0)  # 16 lanes per row
+        _template(W, x, 64, 4, 8, 1, 0)  # 16 lanes per row
     with pytest.raises(RuntimeError, match="rows_per_block must divide threads"):
-        extension().gemv_template(W, x, 64, 3, 8, 1, 0)
+        _template(W, x, 64, 3, 8, 1, 0)
     with pytest.raises(RuntimeError, match="launch failed"):
-        extension().gemv_template(W, x, 64, 1, 3, 1, 0)  # vec 3
+        _template(W, x, 64, 1, 3, 1, 0)  # vec 3
     with pytest.raises(RuntimeError, match="threads"):
-        extension().gemv_template(W, x, 48, 1, 8, 1, 0)
+        _template(W, x, 48, 1, 8, 1, 0)
 
 
 @settings(max_examples=300, deadline=None)
@@ -225,26 +225,26 @@ def test_column_skip_reads_fewer_columns_and_matches_the_model() -> None:
     assert not np.array_equal(got, emulate_column(ColumnConfig(threads=128, vec=8, splits=8), W, x))
 
 
-def test_extension_exposes_the_template_bindings() -> None:
-    from pck.cuda._ext import extension
+def test_native_entries_take_the_pybind_arguments() -> None:
+    """The template launches with the reference's pybind argument lists (bindings.cpp)."""
+    from pck.cuda.template import _column, _template, _template_q8
 
     rng = np.random.default_rng(8)
     W = bf16(rng.standard_normal((64, 700)) * 0.02)
     x = bf16(rng.standard_normal(700))
     Wg, xg = to_gpu(W), to_gpu(x)
-    ext = extension()
     cfg = KernelConfig(threads=128, rows_per_block=2, vec=4, unroll=2, out="bf16")
-    np.testing.assert_array_equal(ext.gemv_template(Wg, xg, 128, 2, 4, 2, 4).cpu().numpy(), emulate(cfg, W, x))
+    np.testing.assert_array_equal(_template(Wg, xg, 128, 2, 4, 2, 4).cpu().numpy(), emulate(cfg, W, x))
     Wq, S = row_q8(W)
     q = KernelConfig(threads=64, vec=2, weights="int8")
-    np.testing.assert_array_equal(ext.gemv_template_q8(Wq, S, xg, 64, 1, 2, 1).cpu().numpy(), emulate(q, W, x))
+    np.testing.assert_array_equal(_template_q8(Wq, S, xg, 64, 1, 2, 1).cpu().numpy(), emulate(q, W, x))
     tickets = torch.zeros(4, dtype=torch.int32, device="cuda")
     c = ColumnConfig(threads=64, vec=2, splits=4)
-    got = ext.gemv_column(to_gpu(W.T), xg, tickets, 64, 2, 4, 0.0).cpu().numpy()
+    got = _column(to_gpu(W.T), xg, tickets, 64, 2, 4, 0.0).cpu().numpy()
     np.testing.assert_array_equal(got, emulate_column(c, W, x))
     assert not tickets.any()
     with pytest.raises(RuntimeError, match="tickets"):
-        ext.gemv_column(to_gpu(W.T), xg, torch.zeros(0, dtype=torch.int32, device="cuda"), 64, 2, 4, 0.0)
+        _column(to_gpu(W.T), xg, torch.zeros(0, dtype=torch.int32, device="cuda"), 64, 2, 4, 0.0)
 
 
 @pytest.mark.parametrize(

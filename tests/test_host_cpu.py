@@ -1,13 +1,12 @@
 """Host-side logic of the pck package that runs without a GPU: the validation the wrappers do
 before any launch (same order and messages as the reference's bindings), the refusal to run
-without the HIP library's device path, round_up_bf16 (reference tests/gpu/test_round_up_bf16.py
-runs on CPU tensors too), the plugin's off switch and its JSONL bookkeeping on CPU tensors."""
+without the HIP library's device path, and round_up_bf16 (reference
+tests/gpu/test_round_up_bf16.py runs on CPU tensors too).  The plugin's host logic is in
+tests/test_plugin_host.py."""
 
 from __future__ import annotations
 
-import json
 import math
-from pathlib import Path
 
 import numpy as np
 import pytest
@@ -18,7 +17,6 @@ from hypothesis import strategies as st
 from pck.cuda import GpuBlockedChecker, check_many, gemv_coalesced, gemv_fp8, gemv_naive
 from pck.cuda.checker import blocked_check, round_up_bf16
 from pck.member import check_members
-from pck.vllm_plugin import CheckStats, register
 
 BF16_MAX = float(torch.finfo(torch.bfloat16).max)
 
@@ -94,44 +92,3 @@ def test_round_up_bf16_overflow_and_errors() -> None:
         round_up_bf16(torch.tensor([1.0]))
 
 
-def test_the_plugin_is_off_unless_enabled(monkeypatch: pytest.MonkeyPatch) -> None:
-    monkeypatch.delenv("PCK_CHECK_SAMPLING", raising=False)
-    register()  # must not import vLLM
-
-
-def _lines(path: Path) -> list[dict]:
-    return [json.loads(line) for line in path.read_text().splitlines()]
-
-
-def test_check_stats_schema_and_flush(tmp_path: Path) -> None:
-    """The JSONL bookkeeping (reference vllm_plugin.py:38-129) on CPU verdict tensors: counts,
-    the -1 'no top-p row' excess, a short run flushed with its pid, idempotent flush."""
-    import os
-
-    log = tmp_path / "check.jsonl"
-    stats = CheckStats(log, every=100)
-    ok = torch.tensor([True, False, True, False])
-    injected = torch.tensor([False, True, False, False])
-    for _ in range(3):
-        stats.add(ok, injected, torch.full((4,), -1.0, dtype=torch.float64))
-    assert not log.exists()
-    stats.flush()
-    last = _lines(log)[-1]
-    assert set(last) == {"rows", "rejected", "injected", "caught", "false_alarms", "steps",
-                         "max_excess", "seconds", "pid", "rank"}  # fmt: skip
-    assert (last["rows"], last["rejected"], last["injected"]) == (12, 6, 3)
-    assert (last["caught"], last["false_alarms"], last["steps"]) == (3, 3, 3)
-    assert last["max_excess"] == -1 and last["pid"] == os.getpid()
-    stats.flush()
-    assert len(_lines(log)) == 1
-
-
-def test_check_stats_writes_every_interval_on_cpu(tmp_path: Path) -> None:
-    log = tmp_path / "check.jsonl"
-    stats = CheckStats(log, every=2)
-    for _ in range(5):
-        stats.add(torch.ones(3, dtype=torch.bool), torch.zeros(3, dtype=torch.bool),
-                  torch.tensor([-1.0, -0.2, -0.5], dtype=torch.float64))  # fmt: skip
-    stats.flush()
-    steps = [line["steps"] for line in _lines(log)]
-    assert steps == [2, 4, 5] and _lines(log)[-1]["max_excess"] == -0.2
