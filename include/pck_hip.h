@@ -259,6 +259,19 @@ int pck_batch_check_workspace(const PckBatchCheckDesc* descs, int count, int64_t
 int pck_batch_check(const PckBatchCheckDesc* descs, int count, void* workspace,
                     int64_t workspace_bytes, void* stream);
 
+/* pck_batch_check without a caller workspace and without any allocation.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops that forbid hipMalloc).  The partial sums go to a file-scope device
+ * array of pck_batch_check_static_bytes() bytes (16 MiB), one per GPU the library runs on,
+ * held until the process ends; its address is looked up once per device, on the first call
+ * with that device current.  A plan that needs more than that returns hipErrorOutOfMemory
+ * (a Llama-3-8B decode layer needs 6.5 MiB at batch 128 or 256); invalid descriptors return
+ * hipErrorInvalidValue as for pck_batch_check; in both cases nothing is enqueued.  Every
+ * call on one GPU shares its array: calls that overlap on one GPU (different streams, or
+ * different host threads) race.  Nothing in the array needs clearing between calls. */
+int64_t pck_batch_check_static_bytes(void);
+int pck_batch_check_static(const PckBatchCheckDesc* descs, int count, void* stream);
+
 /* ---------------------------------------------------------------------------------------------
  * Sampled-token membership check for a batch of rows (top-k / top-p / greedy), the native
  * kernel behind pck.member.check_members (reference src/pck/member.py:118-197).

@@ -46,6 +46,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include <cstdint>
 #include <utility>
 
@@ -482,23 +484,79 @@ extern "C" int pck_batch_check_workspace(const PckBatchCheckDesc* descs, int cou
   return hipSuccess;
 }
 
-extern "C" int pck_batch_check(const PckBatchCheckDesc* descs, int count, void* workspace,
-                               int64_t workspace_bytes, void* stream) {
-  using namespace pck;
-  Plan plan{};
-  const int64_t need = make_plan(descs, count, plan);
-  if (need < 0 || workspace == nullptr || workspace_bytes < need ||
-      reinterpret_cast<uintptr_t>(workspace) % 8 != 0)
-    return hipErrorInvalidValue;
+namespace pck {
+namespace {
+
+// Both launches of a planned check, with the partial sums in `workspace` (at least the plan's
+// bytes, 8-byte aligned; every slot is written by the partial launch before the finish reads
+// it, so it needs no clearing).
+hipError_t launch_planned(Plan& plan, void* workspace, hipStream_t s) {
+  const int count = plan.count;
   plan.part_cx = static_cast<double*>(workspace);
   plan.part_s = plan.part_cx + plan.slots[count];
   const int64_t groups = plan.start[count];
   const int64_t finishers = plan.finish[count];
   if (groups > 0x7FFFFFFF || finishers > 0x7FFFFFFF) return hipErrorInvalidValue;
-  auto s = static_cast<hipStream_t>(stream);
   partial_kernel<<<dim3(static_cast<unsigned>(groups)), dim3(kThreads), 0, s>>>(plan);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   finish_kernel<<<dim3(static_cast<unsigned>(finishers)), dim3(kThreads), 0, s>>>(plan);
   return hipGetLastError();
+}
+
+// The allocation-free entry's workspace: file-scope device memory, one copy on every GPU the
+// library runs on, held until the process ends.  Host code never passes `scratch` itself to a
+// kernel (in host code the name is a stand-in, not a device address): each device's address
+// comes from hipGetSymbolAddress, once per device, with that device current.
+constexpr int64_t kScratchBytes = int64_t{16} << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) double scratch[kScratchBytes / sizeof(double)];
+std::atomic<void*> g_scratch_address[kMaxDevices];
+
+// The current device's address of `scratch` (looked up on this device's first call), or null
+// with the error in `err`.
+void* scratch_address(hipError_t& err) {
+  int device = -1;
+  err = hipGetDevice(&device);
+  if (err != hipSuccess) return nullptr;
+  if (device < 0 || device >= kMaxDevices) {
+    err = hipErrorInvalidDevice;
+    return nullptr;
+  }
+  void* known = g_scratch_address[device].load(std::memory_order_acquire);
+  if (known != nullptr) return known;
+  void* address = nullptr;
+  err = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+  if (err != hipSuccess || address == nullptr) {
+    if (err == hipSuccess) err = hipErrorInvalidSymbol;
+    return nullptr;
+  }
+  g_scratch_address[device].store(address, std::memory_order_release);  // same value if raced
+  return address;
+}
+
+}  // namespace
+}  // namespace pck
+
+extern "C" int pck_batch_check(const PckBatchCheckDesc* descs, int count, void* workspace,
+                               int64_t workspace_bytes, void* stream) {
+  pck::Plan plan{};
+  const int64_t need = pck::make_plan(descs, count, plan);
+  if (need < 0 || workspace == nullptr || workspace_bytes < need ||
+      reinterpret_cast<uintptr_t>(workspace) % 8 != 0)
+    return hipErrorInvalidValue;
+  return pck::launch_planned(plan, workspace, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t pck_batch_check_static_bytes(void) { return pck::kScratchBytes; }
+
+extern "C" int pck_batch_check_static(const PckBatchCheckDesc* descs, int count, void* stream) {
+  pck::Plan plan{};
+  const int64_t need = pck::make_plan(descs, count, plan);
+  if (need < 0) return hipErrorInvalidValue;
+  if (need > pck::kScratchBytes) return hipErrorOutOfMemory;  // beyond the static scratch
+  hipError_t err = hipSuccess;
+  void* workspace = pck::scratch_address(err);
+  if (workspace == nullptr) return err;
+  return pck::launch_planned(plan, workspace, static_cast<hipStream_t>(stream));
 }

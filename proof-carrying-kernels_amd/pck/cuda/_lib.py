@@ -154,6 +154,7 @@ SIGNATURES: dict[str, list[Any]] = {
     "pck_rowsum_check": [ctypes.POINTER(PckRowSumBatch), _p],
     "pck_batch_check_workspace": [ctypes.POINTER(PckBatchCheckDesc), _int, ctypes.POINTER(_i64)],
     "pck_batch_check": [ctypes.POINTER(PckBatchCheckDesc), _int, _p, _i64, _p],
+    "pck_batch_check_static": [ctypes.POINTER(PckBatchCheckDesc), _int, _p],
     "pck_read_stream": [_p, _i64, _p, _int, _p],
     "pck_check_members": [
         _p, _i64, _i64, _p, _p, _p, _p, _f64, _i64, _int, _p, _p, _p, _p,
@@ -168,6 +169,7 @@ SIGNATURES: dict[str, list[Any]] = {
 SIZE_QUERIES: dict[str, list[Any]] = {
     "pck_sampling_scratch_words": [_i64],
     "pck_sampling_partial_bytes": [],
+    "pck_batch_check_static_bytes": [],
 }
 
 

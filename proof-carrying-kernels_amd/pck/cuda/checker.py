@@ -526,41 +526,52 @@ def _batched_kernel_fits(ch: GpuBlockedChecker, X: torch.Tensor, Y: torch.Tensor
     return ch.n % 8 == 0 and ch.block % 4 == 0 and X.data_ptr() % 16 == 0 and Y.data_ptr() % 16 == 0
 
 
+def batched_descriptors(
+    chunk: Sequence[tuple[GpuBlockedChecker, torch.Tensor, torch.Tensor]],
+) -> tuple[Any, list[CheckResult], torch.device]:
+    """Validated launch descriptors (a `PckBatchCheckDesc` array) for up to eight
+    ``(checker, X, Y)`` items, freshly allocated results, and the device."""
+    descs = (PckBatchCheckDesc * len(chunk))()
+    results: list[CheckResult] = []
+    device = None
+    for g, (ch, X, Y) in enumerate(chunk):
+        if device is None:
+            if not Y.is_cuda:
+                raise RuntimeError("Y must be a CUDA tensor")
+            device = Y.device
+        _check_tensor(X, "X", torch.bfloat16, device)
+        _check_tensor(Y, "Y", torch.float32, device)
+        if ch.c.device != device:
+            raise RuntimeError(f"the checker's bank must be on {device}")
+        if not (X.dim() == 2 and X.size(1) == ch.n):
+            raise RuntimeError(f"X must have shape (B, {ch.n}), got {list(X.shape)}")
+        if not (Y.dim() == 2 and Y.size(0) == X.size(0) and Y.size(1) == ch.m):
+            raise RuntimeError(f"Y must have shape ({X.size(0)}, {ch.m}), got {list(Y.shape)}")
+        B = X.size(0)
+        shape = (ch.checks, ch.num_blocks, B)
+        passed = torch.empty(shape, dtype=torch.bool, device=device)
+        rho = torch.empty(shape, dtype=torch.float64, device=device)
+        tau = torch.empty(shape, dtype=torch.float64, device=device)
+        results.append(CheckResult(passed, rho, tau))
+        descs[g] = PckBatchCheckDesc(
+            ch.c.data_ptr(), ch.a.data_ptr(), ch.r.data_ptr(), X.data_ptr(), Y.data_ptr(),
+            passed.data_ptr(), rho.data_ptr(), tau.data_ptr(), ch.n, ch.block,
+            ch.num_blocks, ch.checks, B, ch.coef, ch.geps, ch.tau_floor,
+        )  # fmt: skip
+    assert device is not None
+    if any(X.size(0) == 0 for _, X, _ in chunk):
+        raise RuntimeError("batch size must be positive")
+    return descs, results, device
+
+
 def _check_batched_direct(
     items: Sequence[tuple[GpuBlockedChecker, torch.Tensor, torch.Tensor]],
 ) -> list[CheckResult]:
     results: list[CheckResult] = []
     for i in range(0, len(items), MAX_BATCH):
         chunk = items[i : i + MAX_BATCH]
-        descs = (PckBatchCheckDesc * len(chunk))()
-        device = None
-        for g, (ch, X, Y) in enumerate(chunk):
-            if device is None:
-                if not Y.is_cuda:
-                    raise RuntimeError("Y must be a CUDA tensor")
-                device = Y.device
-            _check_tensor(X, "X", torch.bfloat16, device)
-            _check_tensor(Y, "Y", torch.float32, device)
-            if ch.c.device != device:
-                raise RuntimeError(f"the checker's bank must be on {device}")
-            if not (X.dim() == 2 and X.size(1) == ch.n):
-                raise RuntimeError(f"X must have shape (B, {ch.n}), got {list(X.shape)}")
-            if not (Y.dim() == 2 and Y.size(0) == X.size(0) and Y.size(1) == ch.m):
-                raise RuntimeError(f"Y must have shape ({X.size(0)}, {ch.m}), got {list(Y.shape)}")
-            B = X.size(0)
-            shape = (ch.checks, ch.num_blocks, B)
-            passed = torch.empty(shape, dtype=torch.bool, device=device)
-            rho = torch.empty(shape, dtype=torch.float64, device=device)
-            tau = torch.empty(shape, dtype=torch.float64, device=device)
-            results.append(CheckResult(passed, rho, tau))
-            descs[g] = PckBatchCheckDesc(
-                ch.c.data_ptr(), ch.a.data_ptr(), ch.r.data_ptr(), X.data_ptr(), Y.data_ptr(),
-                passed.data_ptr(), rho.data_ptr(), tau.data_ptr(), ch.n, ch.block,
-                ch.num_blocks, ch.checks, B, ch.coef, ch.geps, ch.tau_floor,
-            )  # fmt: skip
-        assert device is not None
-        if any(X.size(0) == 0 for _, X, _ in chunk):
-            raise RuntimeError("batch size must be positive")
+        descs, res, device = batched_descriptors(chunk)
+        results.extend(res)
         need = ctypes.c_int64(0)
         check(lib().pck_batch_check_workspace(descs, len(chunk), ctypes.byref(need)),
               "batched checker plan")  # fmt: skip
