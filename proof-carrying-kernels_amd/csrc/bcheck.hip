@@ -10,12 +10,14 @@
 // column, which is what this computes, reading the bank once per 32 columns.
 //
 // Arithmetic.
-//   c.x: on the FP64 matrix cores (v_mfma_f64_16x16x4_f64, assumed to round every operation
-//        to nearest as IEEE FP64 does).  c_j x_j has 24 + 8 significand bits, exact in FP64, so
-//        the error of rho stays within the gamma_H(u64) term of the host's geps: a product
-//        passes through at most seg_len / 16 + 3 matrix-core additions, 2 for the workgroup's
-//        K quarters, one per later segment of its subset and 2 for the subsets, and the
-//        subtraction of r . y (itself at most block / 16 + 4 deep), below H >= n + b + 1.
+//   c.x: on the FP64 matrix cores (v_mfma_f64_16x16x4_f64; measured on MI355X with the probe
+//        library: each output is four IEEE FMAs in K order, each rounded once to nearest even,
+//        continued through the accumulator).  c_j x_j has 24 + 8 significand bits, exact in
+//        FP64, so every FMA is one rounded addition and the error of rho stays within the
+//        gamma_H(u64) term of the host's geps: a product passes through at most seg_len / 4
+//        additions in its wave's K quarter, 2 for the workgroup's quarters, one per later
+//        segment of its subset and 2 for the subsets, and the subtraction of r . y (itself at
+//        most block / 16 + 4 deep), below H >= n + b + 1.
 //   s:   on the BF16 matrix cores (v_mfma_f32_16x16x32_bf16, zero accumulator: one step adds 32
 //        exact products a_j |x_j| into an FP32 result) with every step result added in FP64.  A
 //        step's result is below the exact sum of its non-negative products by at most 2^-18

@@ -1,4 +1,6 @@
-"""Builds libpck_hip.so, the gfx950 HIP library behind `pck.cuda` and `pck.member`.
+"""Builds libpck_hip.so, the gfx950 HIP library behind `pck.cuda` and `pck.member`, and
+libpck_probe.so, the probes of device arithmetic that tests run (`pck.cuda.probe`), with the
+same flags.
 
 Run ``python -m pck._build`` (with ``proof-carrying-kernels_amd`` on ``sys.path``) or call
 `build`.  hipcc cross-compiles for gfx950 without a GPU.  The library lands next to this file
@@ -41,6 +43,8 @@ SOURCES = (
     "template.hip",  # the agent's templates: kernels under test, outside the trusted set
     "quantize.hip",  # their INT8 weight copy
 )
+PROBE_LIBRARY = PACKAGE / "libpck_probe.so"
+PROBE_SOURCES = ("probe.hip",)
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -81,23 +85,30 @@ def _compile(src: Path, obj: Path) -> None:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stderr}")
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every source in csrc/ and link libpck_hip.so; returns its path."""
-    out_dir = ROOT / "_build"
-    out_dir.mkdir(exist_ok=True)
-    sources = [CSRC / s for s in SOURCES if (CSRC / s).exists()]
-    objects = [out_dir / (s.stem + ".o") for s in sources]
-    jobs = min(len(sources), max(1, int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
-    with ThreadPoolExecutor(jobs) as pool:
-        list(pool.map(_compile, sources, objects))
-    tmp = LIBRARY.with_suffix(".so.tmp")
+def _link(objects: list[Path], library: Path) -> None:
+    tmp = library.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"linking libpck_hip.so failed:\n{res.stderr}")
-    os.replace(tmp, LIBRARY)
+        raise RuntimeError(f"linking {library.name} failed:\n{res.stderr}")
+    os.replace(tmp, library)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every source in csrc/, link libpck_hip.so and libpck_probe.so; returns the
+    path of libpck_hip.so."""
+    out_dir = ROOT / "_build"
+    out_dir.mkdir(exist_ok=True)
+    names = [s for s in SOURCES + PROBE_SOURCES if (CSRC / s).exists()]
+    sources = [CSRC / s for s in names]
+    objects = {s: out_dir / (Path(s).stem + ".o") for s in names}
+    jobs = min(len(sources), max(1, int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with ThreadPoolExecutor(jobs) as pool:
+        list(pool.map(_compile, sources, [objects[s] for s in names]))
+    _link([objects[s] for s in SOURCES if s in objects], LIBRARY)
+    _link([objects[s] for s in PROBE_SOURCES if s in objects], PROBE_LIBRARY)
     if verbose:
-        print(f"built {LIBRARY}")
+        print(f"built {LIBRARY} and {PROBE_LIBRARY.name}")
     return LIBRARY
 
 

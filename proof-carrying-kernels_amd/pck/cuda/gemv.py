@@ -85,7 +85,9 @@ FP8_MAX = 448.0
 def quantize_fp8(W: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """(Q, s) for `gemv_fp8`: one FP32 scale per row, s = max |w| / 448 (1 for an all-zero
     row), Q = clamp(W / s, +-448) cast to float8_e4m3fn (reference `src/pck/cuda/gemv.py:41-48`).
-    Weight-load preparation; the cast is torch's."""
+    Weight-load preparation in torch ops, as the reference's: the division by the scalar 448 is
+    torch's product with the FP32 reciprocal, W / s is the IEEE FP32 quotient, and the cast
+    rounds to the nearest E4M3 value, ties to even."""
     amax = W.abs().amax(dim=1).float()
     s = torch.where(amax > 0, amax / FP8_MAX, torch.ones_like(amax))
     Q = (W.float() / s[:, None]).clamp(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)

@@ -1,14 +1,21 @@
-"""Writes tests/golden/mfma_step_cases.npz: hardware outputs of single matrix-core steps.
+"""Writes tests/golden/mfma_step_cases.npz: outputs of single matrix-core steps, recorded on an
+MI355X by the probe library (pck.cuda.probe, libpck_probe.so), not by the batched product.
 
 Run on an MI355X from the repository root:
-    python tests/golden/make_mfma_step_fixture.py
-It calls the library's batched product with n = 8, so every output is exactly one populated
-MFMA group with a zero accumulator (one chunk, one K segment; the other segments add -0.0).
-Rows of W and X are crafted pairs (powers of two that probe the truncation window, its sign
-handling, cancellation, significands >= 2 and products in the subnormal range) followed by
-seeded random rows.  Output (b, i) pairs X row b with W row i; the crafted cases sit on the
-diagonal, the off-diagonal outputs are further mixed cases.  The CPU test
-tests/test_oracle_batched.py checks oracle.batched.mfma_step against every kept output.
+    python tests/golden/make_mfma_step_fixture.py [--out PATH]
+
+1. One populated group (W, X, Y_diag, Y_block).  v_mfma_f32_32x32x16_bf16 with lanes 0-31
+   holding 8 K-slots of a 32 x 32 tile and lanes 32-63 zero, zero accumulator: the batched
+   product's step.  Rows of W and X are crafted pairs (powers of two that probe the
+   truncation window, its sign handling, cancellation, significands >= 2 and products in the
+   subnormal range) followed by seeded random rows.  Output (b, i) pairs X row b with W row i;
+   the crafted cases sit on the diagonal, the first 64 W rows against every X row are the
+   block.  The CPU test tests/test_oracle_batched.py checks oracle.batched.mfma_step against
+   every kept output.
+2. Fully populated steps and chains (full_*, chain_*), in the probe's lane order: both lane
+   halves populated with a zero accumulator, and chains of three steps from a nonzero
+   accumulator.  The CPU tests check them against exact sums and a bound, and record that
+   they do not follow the one-group rule extended to two groups.
 """
 
 from __future__ import annotations
@@ -82,26 +89,76 @@ def arrays(seed: int = 7) -> tuple[np.ndarray, np.ndarray]:
     return W, X
 
 
+def tile_operands(W: np.ndarray, X: np.ndarray, ti: int, tb: int) -> tuple[np.ndarray, np.ndarray]:
+    """(a, b) lane operands of one step: lane l < 32 holds W row 32 ti + l and X row
+    32 tb + l (the group's 8 K-slots); lanes 32-63 are zero."""
+    a = np.zeros((64, 8), np.float32)
+    b = np.zeros((64, 8), np.float32)
+    a[:32] = W[32 * ti : 32 * ti + 32]
+    b[:32] = X[32 * tb : 32 * tb + 32]
+    return a, b
+
+
+def output_index(lane: np.ndarray, reg: int) -> tuple[np.ndarray, np.ndarray]:
+    """(row of A, column of B) of result register `reg` in lane `lane` of a 32 x 32 tile."""
+    return 8 * (reg // 4) + 4 * (lane // 32) + reg % 4, lane % 32
+
+
+def chains(seed: int = 9) -> dict[str, np.ndarray]:
+    """Lane-order operands of fully populated steps and of three-step chains."""
+    rng = np.random.default_rng(seed)
+    from pck.fp import bf16
+
+    out = {}
+    for name, steps, tiles in (("full", 1, 8), ("chain", 3, 4)):
+        scale = np.exp2(rng.integers(-12, 13, (2, tiles, steps, 64, 8)) * (rng.random((2, tiles, steps, 64, 1)) < 0.5))
+        out[name + "_a"] = bf16(rng.standard_normal((tiles, steps, 64, 8)) * scale[0])
+        out[name + "_b"] = bf16(rng.standard_normal((tiles, steps, 64, 8)) * scale[1])
+        acc = rng.standard_normal((tiles, 64, 16)) * np.exp2(rng.integers(-8, 9, (tiles, 64, 16)))
+        out[name + "_c"] = (acc * (name == "chain")).astype(np.float32)
+    return out
+
+
 def main() -> None:
+    import argparse
+
     import torch
 
-    from pck.cuda import gemm_batched
+    from pck.cuda import probe
 
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--out", type=Path, default=OUT)
+    args = ap.parse_args()
     W, X = arrays()
-    Wt = torch.from_numpy(W).to(torch.bfloat16).cuda()
-    Xt = torch.from_numpy(X).to(torch.bfloat16).cuda()
-    Y = gemm_batched(Wt, Xt)
+    dev = lambda v: torch.from_numpy(np.ascontiguousarray(v, np.float32)).to(torch.bfloat16).cuda()  # noqa: E731
+    tiles = [(t, t) for t in range(W.shape[0] // 32)] + [(ti, tb) for ti in range(BLOCK // 32)
+                                                         for tb in range(X.shape[0] // 32)]  # fmt: skip
+    ops = [tile_operands(W, X, ti, tb) for ti, tb in tiles]
+    a = np.stack([o[0] for o in ops])[:, None]
+    b = np.stack([o[1] for o in ops])[:, None]
+    d = probe.mfma_bf16(dev(a), dev(b), torch.zeros((len(tiles), 64, 16), device="cuda")).cpu().numpy()
+    Y = np.full((X.shape[0], W.shape[0]), np.nan, np.float32)  # Y[b, i]
+    lanes = np.arange(64)
+    for k, (ti, tb) in enumerate(tiles):
+        for reg in range(16):
+            i, j = output_index(lanes, reg)
+            Y[32 * tb + j, 32 * ti + i] = d[k, :, reg]
+    extra = chains()
+    for name in ("full", "chain"):
+        extra[name + "_d"] = probe.mfma_bf16(dev(extra[name + "_a"]), dev(extra[name + "_b"]),
+                                             torch.from_numpy(extra[name + "_c"]).cuda()).cpu().numpy()  # fmt: skip
     torch.cuda.synchronize()
-    save(W, X, Y.cpu().numpy(), torch.cuda.get_device_name())
+    save(args.out, W, X, Y, torch.cuda.get_device_name(), extra)
 
 
-def save(W: np.ndarray, X: np.ndarray, Y: np.ndarray, device: str) -> None:
+def save(out: Path, W: np.ndarray, X: np.ndarray, Y: np.ndarray, device: str,
+         extra: dict[str, np.ndarray]) -> None:  # fmt: skip
     """Keeps the diagonal (the crafted cases) and the first 64 weight rows against every batch
-    row: Y_diag[c] = Y[c, c], Y_block = Y[:, :64]."""
-    np.savez_compressed(
-        OUT, W=W, X=X, Y_diag=np.diagonal(Y).copy(), Y_block=Y[:, :BLOCK].copy(), device=device
-    )
-    print(f"wrote {OUT} ({W.shape[0]} diagonal + {Y.shape[0]} x {BLOCK} outputs)")
+    row: Y_diag[c] = Y[c, c], Y_block = Y[:, :64]; and the lane-order chain records."""
+    diag, block = np.diagonal(Y).copy(), Y[:, :BLOCK].copy()
+    assert not np.isnan(diag).any() and not np.isnan(block).any()
+    np.savez_compressed(out, W=W, X=X, Y_diag=diag, Y_block=block, device=device, **extra)
+    print(f"wrote {out} ({W.shape[0]} diagonal + {Y.shape[0]} x {BLOCK} outputs, chains)")
 
 
 if __name__ == "__main__":

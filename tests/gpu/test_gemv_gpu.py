@@ -300,6 +300,53 @@ def test_quantize_fp8_scales_rows() -> None:
     assert rel < 0.05
 
 
+def nearest_e4m3_codes(v: NDArray[np.float32]) -> NDArray[np.uint8]:
+    """Brute force over the 254 finite codes of `oracle.gemv.e4m3_values`: the code nearest to
+    each FP32 value (|v| <= 448), ties to the code with an even mantissa, zeros keeping the
+    sign of v."""
+    table = e4m3_values().astype(np.float64)
+    codes = np.array([c for c in range(256) if np.isfinite(table[c])])
+    dist = np.abs(v.astype(np.float64)[:, None] - table[codes][None, :])
+    best = dist.min(axis=1, keepdims=True)
+    tied = dist == best
+    even = (codes & 1) == 0
+    sign_match = ((codes & 0x80) != 0)[None, :] == np.signbit(v)[:, None]
+    score = tied * (4 + 2 * even[None, :] + sign_match)  # nearest first, then even, then sign
+    return codes[score.argmax(axis=1)].astype(np.uint8)
+
+
+def test_quantize_fp8_codes_are_the_nearest_e4m3() -> None:
+    """Q's bits against a brute-force nearest-E4M3 (ties to even) of W / s, with
+    s = max|w| * fl(1 / 448) and W / s IEEE FP32 operations: row 0 (max 448, so s = 1) holds every finite E4M3 value, every
+    midpoint between neighbours (exact ties, including the subnormal range and 0), and the
+    BF16 values just beside each midpoint; the other rows are seeded at several scales."""
+    table = e4m3_values()
+    pos = np.unique(table[np.isfinite(table) & (table >= 0)])
+    mids = (pos[:-1] + pos[1:]) / 2  # 4 significant bits: BF16-exact
+    beside = np.concatenate([np.nextafter(mids, 0), np.nextafter(mids, 1)])
+    special = np.concatenate([pos, mids, bf16(beside), [2.0**-11, 2.0**-10, 3 * 2.0**-11]])
+    special = np.concatenate([special, -special])
+    n = special.size + (-special.size) % 16
+    rng = np.random.default_rng(4)
+    rows = [np.concatenate([special, np.zeros(n - special.size)])]
+    for scale in (1e-6, 0.02, 1.0, 300.0, 2.0**40, 2.0**-100):
+        for _ in range(3):
+            rows.append(rng.standard_normal(n) * scale)
+    W = bf16(np.stack(rows)).astype(np.float32)
+    assert np.abs(W[0]).max() == 448.0
+    Q, s = quantize_fp8(torch.from_numpy(W).to(torch.bfloat16).cuda())
+    amax = np.abs(W).max(axis=1)
+    # torch divides a tensor by a Python scalar as a product with the FP32 reciprocal
+    inv = np.float32(1.0) / np.float32(448.0)
+    s_ref = np.where(amax > 0, amax * inv, np.float32(1.0)).astype(np.float32)
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    v = np.clip(W / s_ref[:, None], -448.0, 448.0).astype(np.float32)
+    want = nearest_e4m3_codes(v.ravel()).reshape(v.shape)
+    got = Q.view(torch.uint8).cpu().numpy()
+    np.testing.assert_array_equal(got, want)
+    assert (v[0] != 0).sum() > 1000 and len(np.unique(got[0])) == 254
+
+
 def test_fp8_rejects_bf16_weights() -> None:
     W, x = fp8_problem(4, 32, seed=0)
     with pytest.raises(RuntimeError, match="Float8_e4m3fn"):

@@ -1,6 +1,7 @@
 """The C ABI of libpck_hip.so, checked without a GPU: the library loads, exports every function
-include/pck_hip.h declares, and the ctypes mirrors of its structs have the header's layout
-(gcc compiles the header and prints sizeof / offsetof)."""
+the headers under include/ declare (include/pck_probe.h: libpck_probe.so, the probes of device
+arithmetic), and the ctypes mirrors of its structs have the header's layout (gcc compiles the
+header and prints sizeof / offsetof)."""
 
 from __future__ import annotations
 
@@ -18,10 +19,13 @@ HEADER = ROOT / "include" / "pck_hip.h"
 HEADERS = sorted((ROOT / "include").glob("*.h"))
 
 
-def declared_functions() -> list[str]:
-    """Every pck_* function that a header under include/ declares."""
+PROBE_HEADER = ROOT / "include" / "pck_probe.h"
+
+
+def declared_functions(headers: list[Path] | None = None) -> list[str]:
+    """Every pck_* function that the headers (default: those of libpck_hip.so) declare."""
     names: set[str] = set()
-    for header in HEADERS:
+    for header in headers if headers is not None else [h for h in HEADERS if h != PROBE_HEADER]:
         text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
         names |= set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(pck_\w+)\s*\(", text, flags=re.M))
     return sorted(names)
@@ -56,6 +60,18 @@ def test_library_exports_every_declared_function() -> None:
     from pck.cuda import template
 
     assert set(declared_functions()) >= set(template.SIGNATURES) | {"pck_column_tiles"}
+
+
+def test_probe_library_exports_its_header() -> None:
+    from pck.cuda import probe
+
+    names = declared_functions([PROBE_HEADER])
+    assert set(names) == set(probe.SIGNATURES)
+    handle = probe.lib()
+    for name in names:
+        assert hasattr(handle, name), name
+    subprocess.run(["gcc", "-std=c11", "-fsyntax-only", "-Wall", "-Werror", "-x", "c",
+                    str(PROBE_HEADER)], check=True)  # fmt: skip
 
 
 def test_template_header_compiles_as_c_and_argument_counts_match(tmp_path: Path) -> None:
