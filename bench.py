@@ -48,6 +48,7 @@ import statistics
 import sys
 import time
 from pathlib import Path
+from typing import Any
 
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "proof-carrying-kernels_amd"))
@@ -698,22 +699,31 @@ def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: in
 
             by_launch: dict[str, list[int]] = {}
 
-            def tally(kind: str, v: torch.Tensor) -> None:
-                # v: (num_blocks, B) verdicts; a column (one GEMV output, the reference's unit
-                # in harness/real_activations.py:144-165) is caught if any of its blocks fails
+            escaped: dict[str, list[float]] = {}
+
+            def tally(kind: str, res: Any) -> None:
+                # verdicts (num_blocks, B); a column (one GEMV output, the reference's unit in
+                # harness/real_activations.py:144-165) is caught if any of its blocks fails.
+                # An escaped column's largest |rho| / tau over its blocks says how far below
+                # the threshold its error stayed.
+                v = res.verdict
                 c = kinds.setdefault(kind, [0, 0, 0, 0])
                 c[0] += int((~v).sum())
                 c[1] += v.numel()
                 c[2] += int((~v).any(dim=0).sum())
                 c[3] += v.size(1)
                 by_launch.setdefault(kind, []).append(int((~v).any(dim=0).sum()))
+                missed = ~(~v).any(dim=0)
+                if bool(missed.any()):
+                    ratio = (res.rho.abs() / res.tau).amax(dim=(0, 1))[missed]
+                    escaped.setdefault(kind, []).extend(round(float(r), 4) for r in ratio.tolist())
 
             for idx, ((_, ch), X, Y) in enumerate(zip(ls[0], xs, ys)):
                 honest = ch.check_batched(X, Y).verdict
                 false_alarms += int((~honest).sum())
                 cells += honest.numel()
                 m, n = Y.size(1), X.size(1)
-                tally("bf16_output", ch.check_batched(X, Y.to(torch.bfloat16).float()).verdict)
+                tally("bf16_output", ch.check_batched(X, Y.to(torch.bfloat16).float()))
                 for bit, kind in ((30, "exponent_flip"), (31, "sign_flip")):
                     # top exponent bit of a random output / sign of the block's largest output
                     y = Y.clone()
@@ -725,25 +735,25 @@ def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: in
                     rows = sel + torch.arange(0, m, BLOCK, device=y.device)
                     bits = y.view(torch.int32)
                     bits.scatter_(1, rows, bits.gather(1, rows) ^ (1 << bit))
-                    tally(kind, ch.check_batched(X, y).verdict)
+                    tally(kind, ch.check_batched(X, y))
                 Wq = quantize_fp8(raw[0][idx])[0] if fp8 else raw[0][idx]
                 Wf = (Wq.float() if not fp8 else Wq.to(torch.float32)).t()  # (n, m)
                 Xf = X.float()
                 # dropped tail: the product skips the last 4 columns of every reduction
                 Wz = Wq.clone()
                 Wz.view(torch.uint8 if fp8 else torch.int16)[:, -4:] = 0
-                tally("skip_tail_4", ch.check_batched(X, gemm_batched(Wz, X)).verdict)
+                tally("skip_tail_4", ch.check_batched(X, gemm_batched(Wz, X)))
                 # BF16 partials: the 8 K segments' sums rounded to BF16 before they are added
                 seg = -(-n // 8)
                 yp = torch.zeros_like(Y)
                 for j in range(0, n, seg):
                     yp += (Xf[:, j : j + seg] @ Wf[j : j + seg]).to(torch.bfloat16).float()
-                tally("bf16_partials", ch.check_batched(X, yp).verdict)
+                tally("bf16_partials", ch.check_batched(X, yp))
                 # BF16 accumulator: the running sum rounded to BF16 after every 32 columns
                 ya = torch.zeros_like(Y)
                 for j in range(0, n, 32):
                     ya = (ya + Xf[:, j : j + 32] @ Wf[j : j + 32]).to(torch.bfloat16).float()
-                tally("bf16_accumulator", ch.check_batched(X, ya).verdict)
+                tally("bf16_accumulator", ch.check_batched(X, ya))
             planted = sum(c[3] for c in kinds.values())
             caught = sum(c[2] for c in kinds.values())
             key = "fp8" if fp8 else "bf16"
@@ -762,6 +772,7 @@ def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: in
                         "columns_caught_per_launch": dict(zip([x[0] for x in BATCHED_LAUNCHES], by_launch[k]))}
                     for k, (c, p, cc, cp) in kinds.items()
                 },
+                "escaped_columns_max_rho_over_tau": escaped,
                 "false_alarms": false_alarms,
                 "honest_cells": cells,
             }
@@ -1089,6 +1100,7 @@ def main() -> None:
             key: {w: {"products_ms": e[w]["gemm_only_ms"], "checker_overhead_pct": e[w]["checker_overhead_pct"],
                       "mfma_peak_frac": e[w]["mfma_peak_frac"],
                       "faulty_columns_caught": f"{e[w]['faulty_columns_caught']}/{e[w]['faulty_columns']}",
+                      "escaped_max_rho_over_tau": e[w]["escaped_columns_max_rho_over_tau"],
                       "false_alarms": e[w]["false_alarms"]} for w in ("bf16", "fp8")}
                  | {"hipblaslt_ms": e["hipblaslt_ms_per_layer"]}
             for key, e in batched.items()

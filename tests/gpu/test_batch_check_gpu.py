@@ -1,6 +1,8 @@
 """The batched blocked checker (every column of Y = X W^T checked) against the oracle: verdicts
 equal to the CPU reference checker, column by column, on the same (W, X[b], Y[b], r) for honest
-and faulty outputs; equal to the single-vector HIP checker; tau within [exact threshold,
+and faulty outputs (for the reference's BF16-accumulator and BF16-partials shortcuts at the
+down projection's full size, BF16 and FP8, except in the band just above the CPU's tau that the
+BF16 rounding of the GPU bank's a opens); equal to the single-vector HIP checker; tau within [exact threshold,
 exact (1 + 2^-15)] (the BF16 matrix-core bound of a . |x|) and never below the exact threshold
 when X spans subnormals to large values; rho within its proven rounding; honest batched
 products at Llama-3-8B shapes pass with the batched tree height."""
@@ -100,6 +102,69 @@ def test_verdicts_equal_the_cpu_reference_column_by_column(kind: str) -> None:
         assert not gpu.all()  # an error near tau per check: most cells, not every one
     else:
         assert not gpu.any()
+
+
+def shortcut(kind: str, Wq: torch.Tensor, X: torch.Tensor) -> torch.Tensor:
+    """A batched product with a reduced-precision shortcut, from FP32 products of the exact
+    weight values: ``bf16_partials`` rounds each of the 8 K segments' sums to BF16 before
+    adding them; ``bf16_accumulator`` rounds the running sum to BF16 after every 32 columns."""
+    Wf = Wq.float().t().contiguous()  # (n, m), exact E4M3 / BF16 values
+    Xf = X.float()
+    n = Xf.size(1)
+    Y = torch.zeros((Xf.size(0), Wf.size(1)), dtype=torch.float32, device=X.device)
+    if kind == "bf16_partials":
+        seg = -(-n // 8)
+        for j in range(0, n, seg):
+            Y += (Xf[:, j : j + seg] @ Wf[j : j + seg]).to(torch.bfloat16).float()
+    else:
+        for j in range(0, n, 32):
+            Y = (Y + Xf[:, j : j + 32] @ Wf[j : j + 32]).to(torch.bfloat16).float()
+    return Y
+
+
+@pytest.mark.parametrize("fp8", [False, True], ids=["bf16", "fp8"])
+@pytest.mark.parametrize("kind", ["bf16_accumulator", "bf16_partials"])
+def test_shortcuts_at_the_down_projection(kind: str, fp8: bool) -> None:
+    """The reference's BF16-accumulator and BF16-partials shortcuts planted in batched outputs of
+    Llama-3-8B's down projection (4096 x 14336), BF16 and FP8 weights, b = 128: honest outputs
+    pass, and the batched checker's verdicts equal the CPU reference column by column except
+    where the CPU's |rho| lies just above its own tau: the GPU bank rounds a up to BF16 (as
+    the reference's GPU bank does, `cuda/checker.py:99-101`) where the CPU checker rounds it up
+    to FP32, so the GPU tau may be up to 2^-8 larger and pass such a cell.  The largest
+    |rho| / tau over a column's blocks is reported for the column nearest to escaping (an
+    error below tau in every block is the bound's floor: T2 promises detection above 2 tau).
+    """
+    m, n, B = 4096, 14336, 48
+    g = torch.Generator().manual_seed(1 + fp8)
+    W = (torch.randn(m, n, generator=g) * 0.02).to(torch.bfloat16).cuda()
+    Wq = quantize_fp8(W)[0] if fp8 else W
+    Wc = Wq.to(torch.bfloat16)  # the weights' exact values
+    X = torch.randn(B, n, generator=g).to(torch.bfloat16).cuda()
+    height = batched_height(n)
+    checker = GpuBlockedChecker(Wc, 128, height, generator=torch.Generator().manual_seed(5))
+    print(f"batched shortcut {kind} fp8={fp8} m={m} n={n} B={B}", flush=True)
+    honest = checker.check_batched(X, gemm_batched(pack_batched_weights(Wq), X))
+    assert bool(honest.verdict.all())
+    Y = shortcut(kind, Wq, X)
+    res = checker.check_batched(X, Y)
+    gpu = res.verdict.cpu().numpy()
+    W_np, X_np, Y_np = Wc.float().cpu().numpy(), X.float().cpu().numpy(), Y.cpu().numpy()
+    bank = WeightBank(W_np, 128)
+    signs = checker.r.cpu().numpy().astype(np.float64)
+    cpu_pass, cpu_ratio = [], []
+    for b in range(B):
+        passed, rho, tau = BlockedChecker(W_np, X_np[b], 128, height, bank=bank).verdict_with_signs(Y_np[b], signs)
+        cpu_pass.append(passed.all(0))
+        cpu_ratio.append((np.abs(rho) / tau).max(0))
+    cpu, cpu_r = np.stack(cpu_pass, 1), np.stack(cpu_ratio, 1)
+    band = ~cpu & gpu & (cpu_r <= 1 + 2.0**-7)
+    assert ((gpu == cpu) | band).all()
+    print(f"  cells {gpu.size}, verdicts differing in the a-rounding band {int(band.sum())}", flush=True)
+    ratio = (res.rho.abs() / res.tau).amax(dim=(0, 1))  # per column: its largest block ratio
+    caught = int((~res.verdict).any(dim=0).sum())
+    print(f"  columns caught {caught}/{B}; smallest column max |rho|/tau {float(ratio.min()):.3g}",
+          flush=True)  # fmt: skip
+    assert caught >= B - 2 and bool(((ratio > 1) == (~res.verdict).any(dim=0)).all())
 
 
 def test_batched_equals_the_single_vector_checker() -> None:
