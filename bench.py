@@ -551,6 +551,94 @@ def membership(copies: int = 4, reps: int = 20) -> dict:
     }
 
 
+def plugin_step(reps: int = 50) -> dict:
+    """Per-step cost of the vLLM plugin's wrapper (`pck.vllm_plugin.install`) at B = 256,
+    V = 151,936 (config 5).  A scripted stand-in with vLLM 0.33's ``_sample_random`` signature
+    returns fixed tokens (the argmax of each row), so the difference between the wrapped and
+    the bare method is the wrapper: the copy of the logits, one membership launch that adds
+    into the device totals, and the host bookkeeping.  Times are wall clock over ``reps``
+    back-to-back steps (host issue and device work together), plus the host time to issue
+    them and event times of the copy and of the membership launch alone.  The reference
+    measured its wrapper inside a real vLLM decode step: 22.1% of the step, about 0.9 ms of
+    dispatch (harness/bench_vllm_checker_out.txt:4-5); vLLM is not installed here."""
+    import json as _json
+    import tempfile
+    from types import SimpleNamespace
+
+    import numpy as np
+    import torch
+
+    from pck.member import launch_check, new_totals
+    from pck.vllm_plugin import install
+
+    rows, vocab = 256, 151_936
+    dev = torch.device("cuda")
+    g = torch.Generator(device="cuda").manual_seed(1)
+    logits = torch.randn(rows, vocab, generator=g, device=dev) * 3
+    tokens = logits.argmax(dim=1)
+    top_k = torch.full((rows,), 50, dtype=torch.long, device=dev)
+    top_p = torch.full((rows,), 0.9, dtype=torch.float32, device=dev)
+    temperature = torch.ones(rows, dtype=torch.float32, device=dev)
+    idx = torch.arange(rows, device=dev)
+    idx_np = np.arange(rows)
+
+    class Scripted:
+        sampling_states = SimpleNamespace(temperature=SimpleNamespace(gpu=temperature),
+                                          top_k=SimpleNamespace(np=np.full(rows, 50)))  # fmt: skip
+
+        def _sample_random(self, lg, ix, ix_np, pos, tk, tp, topp_only, fused):  # type: ignore[no-untyped-def]
+            return tokens, lg
+
+    log = Path(tempfile.mkdtemp()) / "pck_sampling_check.jsonl"
+    wrapped_cls = type("Wrapped", (Scripted,), {})
+    stats = install(wrapped_cls, log, every=16)
+
+    def steps(sampler, n: int) -> tuple[float, float]:  # type: ignore[no-untyped-def]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            sampler._sample_random(logits, idx, idx_np, idx, top_k, top_p, False, False)
+        issued = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n * 1e3, issued / n * 1e3
+
+    def events(fn, n: int) -> float:  # type: ignore[no-untyped-def]
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(n):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / n
+
+    bare, wrapped = Scripted(), wrapped_cls()
+    steps(bare, 5)
+    steps(wrapped, 5)
+    bare_ms = statistics.median(steps(bare, reps)[0] for _ in range(5))
+    runs = [steps(wrapped, reps) for _ in range(5)]
+    wrapped_ms = statistics.median(r[0] for r in runs)
+    issue_ms = statistics.median(r[1] for r in runs)
+    totals = new_totals(dev)
+    check_ms = events(lambda: launch_check(logits, tokens, top_k, top_p, None, 1e-4, np.full(rows, 50),
+                                           temperature=temperature, temperature_index=idx,
+                                           totals=totals, outputs=False), reps)  # fmt: skip
+    clone_ms = events(lambda: logits.clone(), reps)
+    stats.flush()
+    last = _json.loads(log.read_text().splitlines()[-1])
+    assert last["rows"] == stats.steps * rows and last["rejected"] == 0, last
+    return {
+        "workload": "vLLM 0.33 _sample_random stand-in, 256 x 151936 fp32 logits, top-k 50, top-p 0.9",
+        "wrapper_ms_per_step": round(wrapped_ms - bare_ms, 5),
+        "wrapped_step_ms": round(wrapped_ms, 5),
+        "bare_step_ms": round(bare_ms, 5),
+        "host_issue_ms_per_step": round(issue_ms, 5),
+        "check_members_ms": round(check_ms, 5),
+        "logits_copy_ms": round(clone_ms, 5),
+        "steps_logged": last["steps"],
+        "reference": "22.1% of a vLLM decode step, ~0.9 ms dispatch (harness/bench_vllm_checker_out.txt:4-5)",
+    }
+
+
 SAMPLING_REFERENCE_MS = {  # harness/bench_sampling_out.txt:6-13 (RTX 5060, cold L2, median)
     "B1": {"topk_checker": 0.0253, "topp_checker": 0.0666},
     "B8": {"topk_checker": 0.0378, "topp_checker": 0.1649},
@@ -986,8 +1074,9 @@ def main() -> None:
         help="fewest rounds, no eager timing, no CPU baseline (for counter collection)",
     )  # fmt: skip
     parser.add_argument(
-        "--section", choices=("all", "b1", "templates"), default="all",
-        help="b1: only the batch-1 layer (BF16 and FP8); templates: only the agent's templates",
+        "--section", choices=("all", "b1", "templates", "members"), default="all",
+        help="b1: only the batch-1 layer (BF16 and FP8); templates: only the agent's templates; "
+             "members: only the membership check and the vLLM plugin's step",
     )  # fmt: skip
     args = parser.parse_args()
     if args.quick:
@@ -1003,6 +1092,9 @@ def main() -> None:
 
     if args.section == "templates":
         print(json.dumps({"templates": templates_layer()}), flush=True)
+        return
+    if args.section == "members":
+        print(json.dumps({"membership": membership(), "vllm_plugin": plugin_step()}), flush=True)
         return
     depth = 32  # a Llama-3-8B decode pass
     # At least 7 alternating rounds whatever --steps is; each round replays one 32-layer pass
@@ -1031,17 +1123,20 @@ def main() -> None:
             for kind, w in (("bf16", 2), ("fp8", 1))
         },
     }
-    member = sampling = batched = templates = None
+    member = plugin = sampling = batched = templates = None
     if args.section == "all":
         print("[bench] timing the membership check", file=sys.stderr, flush=True)
         member = membership()
+        print("[bench] timing the vLLM plugin's wrapper per step", file=sys.stderr, flush=True)
+        plugin = plugin_step()
         print("[bench] timing the set-sampling checker", file=sys.stderr, flush=True)
         sampling = sampling_checker(50 if args.quick else 200)
         print("[bench] timing the batched layer (B = 128, 256)", file=sys.stderr, flush=True)
         batched = batched_layer()
         print("[bench] timing the agent's GEMV templates", file=sys.stderr, flush=True)
         templates = templates_layer()
-        detail |= {"membership": member, "sampling": sampling, "batched": batched, "templates": templates}
+        detail |= {"membership": member, "vllm_plugin": plugin, "sampling": sampling, "batched": batched,
+                   "templates": templates}  # fmt: skip
 
     # The headline: the batch-1 BF16 layer with every output checked, in the fastest checked
     # mode (bank checks carried in later GEMV launches, b = 128).
@@ -1095,6 +1190,9 @@ def main() -> None:
     }
     if member is not None:
         line["membership"] = {k: member[k] for k in ("ms", "gbps", "pct_of_peak", "planted_caught", "false_alarms")}
+    if plugin is not None:
+        line["vllm_plugin"] = {k: plugin[k] for k in ("wrapper_ms_per_step", "host_issue_ms_per_step",
+                                                      "check_members_ms", "logits_copy_ms")}  # fmt: skip
     if batched is not None:
         line["batched"] = {
             key: {w: {"products_ms": e[w]["gemm_only_ms"], "checker_overhead_pct": e[w]["checker_overhead_pct"],
