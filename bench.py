@@ -159,16 +159,22 @@ def run_step(layer, with_check: bool, events=None):  # type: ignore[no-untyped-d
 MODES = ("gemv", "serial", "side_stream", "carried", "carried_b256", "inpass", "inpass_b256",
          "inpass_sums")  # fmt: skip
 
-# In the carried and in-pass modes the long launches of layer L also check outputs finished by
-# earlier launches: gate_up carries the previous layer's down and this layer's q, k, v, o; down
-# carries gate and up; q/k/v and o carry nothing; the pass ends with one standalone check of
-# the last down.  ("prev", name) refers to the previous layer's output.
+# In the carried and in-pass modes the gate_up launch of layer L also checks every output
+# finished since the previous gate_up: the previous layer's gate, up and down and this layer's
+# q, k, v and o; the other launches carry nothing, and the pass ends with one standalone check
+# of the last layer's gate, up and down.  ("prev", name) refers to the previous layer's output.
+# gate_up is the launch with many more workgroups than the GPU holds at once (3,584 at
+# threads 256), so the dispatcher fills the CUs that finish early and the carried checks add
+# about their bytes; in a launch that fits in one round (down: 512), each CU that hosts a
+# check finishes last and the launch waits for it.
 CARRIES = {
     "qkv": (),
     "o": (),
-    "gate_up": (("prev", "down"), ("this", "q"), ("this", "k"), ("this", "v"), ("this", "o")),
-    "down": (("this", "gate"), ("this", "up")),
+    "gate_up": (("prev", "gate"), ("prev", "up"), ("prev", "down"), ("this", "q"), ("this", "k"),
+                ("this", "v"), ("this", "o")),
+    "down": (),
 }
+LAST_CHECKED = ("gate", "up", "down")  # the pass's final standalone check
 
 
 def carried_pass(layers, depth: int, block: int, inpass: bool, checks: bool = True):  # type: ignore[no-untyped-def]
@@ -203,9 +209,11 @@ def carried_pass(layers, depth: int, block: int, inpass: bool, checks: bool = Tr
     if checks:
         owner, produced, produced_sums = prev
         if inpass:
-            results.extend(rowsum_check_many([(owner["down"]["rows"][block], produced_sums["down"], produced["down"])]))
+            results.extend(rowsum_check_many([(owner[n]["rows"][block], produced_sums[n], produced[n])
+                                              for n in LAST_CHECKED]))  # fmt: skip
         else:
-            results.extend(check_many([(owner["down"]["bank"][block], owner["down"]["x"], produced["down"])]))
+            results.extend(check_many([(owner[n]["bank"][block], owner[n]["x"], produced[n])
+                                       for n in LAST_CHECKED]))  # fmt: skip
     return results
 
 
@@ -1074,9 +1082,10 @@ def main() -> None:
         help="fewest rounds, no eager timing, no CPU baseline (for counter collection)",
     )  # fmt: skip
     parser.add_argument(
-        "--section", choices=("all", "b1", "templates", "members"), default="all",
+        "--section", choices=("all", "b1", "templates", "members", "batched"), default="all",
         help="b1: only the batch-1 layer (BF16 and FP8); templates: only the agent's templates; "
-             "members: only the membership check and the vLLM plugin's step",
+             "members: only the membership check and the vLLM plugin's step; batched: only the "
+             "batched layer (B = 128, 256)",
     )  # fmt: skip
     args = parser.parse_args()
     if args.quick:
@@ -1095,6 +1104,9 @@ def main() -> None:
         return
     if args.section == "members":
         print(json.dumps({"membership": membership(), "vllm_plugin": plugin_step()}), flush=True)
+        return
+    if args.section == "batched":
+        print(json.dumps({"batched": batched_layer(reps=3 if args.quick else 7)}), flush=True)
         return
     depth = 32  # a Llama-3-8B decode pass
     # At least 7 alternating rounds whatever --steps is; each round replays one 32-layer pass
