@@ -8,19 +8,30 @@ N(0, 0.02) BF16, x ~ N(0, 1) BF16) and rotate over several distinct layer copies
 exceeds L2 + MALL, so every step streams its weights from HBM, as decoding through a model does.
 
 A 32-layer decode pass (the depth of Llama-3-8B) cycling over the layer copies is captured once
-in a HIP graph and replayed, as a decode loop replays its captured model (eager Python launches
-leave the GPU idle between kernels; their per-step time is reported beside).  The passes of the
-four modes below are replayed in alternating rounds, steps / 32 rounds of one pass each, and
-each figure is the median round.  Every GEMV output
-is checked by the trusted blocked checker in a later launch of the same stream: the checker's
-workgroups ride in a later GEMV launch (pck_gemv_group_check; bit-identical to a standalone
-check), the long gate/up and down launches, so their latency hides behind the weight stream.  The same pass with one standalone
-checker launch per layer (the reference's batched mode) is reported as
-checker_overhead_serial_pct, and with that launch on a side stream as
-checker_overhead_side_stream_pct.
+in a HIP graph per mode and replayed, as a decode loop replays its captured model.  The modes
+are replayed in alternating rounds, max(7, steps / 32) rounds whatever --steps is (3 with
+--quick), and each figure is the median round.  Modes (BF16 and FP8 layers):
+  gemv_only          the four launches, nothing checked
+  carried (b = 128, 256)  every output checked by the bank checker inside the next layer's
+                     gate/up launch (pck_gemv_group_check, bit-identical to a standalone check);
+                     the pass ends with one standalone check of the last gate, up and down
+  inpass (b = 128, 256)   the GEMVs also write per-row checksums in the same pass
+                     (pck_gemv_group_rowsums) and the row-sum checks ride as above
+  serial, side_stream     one standalone check per layer, inline or on a second stream
+The headline `value` is the carried mode at b = 128.  A B = 1 fault campaign plants the
+reference's shortcuts (dropped tail, BF16 accumulator / partials / output) and per-block
+exponent and sign flips in every output of one layer and reports caught outputs and false
+alarms for the bank and row-sum checks at b = 128 and 256.
 
-Printed JSON line:
+Printed: one compact JSON line on stdout (the contract line) and the full per-section figures
+as one `[bench detail]` JSON line on stderr.  The contract line holds:
   value          GEMV algorithmic bytes per step / time per replayed step, checker included
+  checker_overhead_pct, fp8_checker_overhead_pct   every mode above against gemv_only
+  faults_b1      the campaign's caught outputs and false alarms
+  membership     the top-k / top-p membership check, 256 x 151,936 logits
+  vllm_plugin    the plugin wrapper's cost per step at the same size, beside the check alone
+  batched        B = 128 and 256: products, checker overhead, caught faulty columns (with the
+                 largest |rho| / tau of any column that escaped), hipBLASLt's time
   roofline       the dominant kernel (the BF16 tree GEMV instance used by q/k/v, o, gate/up):
                  algorithmic bytes per launch / its mean launch duration, from HIP events on
                  the launch stream around a graph that replays those launches back to back
@@ -29,14 +40,14 @@ Printed JSON line:
                  the committed summary named by traffic_source
   cpu_baseline   the oracle's CPU model of the same work (coalesced-tree GEMV + CPU blocked
                  checker) timed on this host on a bounded sample, one core (the all-core C
-                 model in cpu_baseline_all_cores, the FP8 layer in fp8.cpu_baseline)
-plus the FP8 layer, GEMV-only times, the checker overhead, the membership check (256 x 151936
-logits), the set-sampling checker, the batched layer (B = 128, 256), the agent's GEMV templates
-over the same layer (row-major, INT8 and column-major configs) and the read-only stream
-ceilings: the long stream (hbm_read_ceiling_gbps) and one launch over each GEMV launch's bytes
-(size_matched_read_us; pct_of_size_matched_read is their sum over the layer's time).
+                 model in cpu_baseline_all_cores_gbps, the FP8 layer in fp8_cpu_baseline_gbps)
+The detail line adds the set-sampling checker, the agent's GEMV templates over the same layer
+and the read-only stream ceilings: the long stream (hbm_read_ceiling_gbps) and one launch over
+each GEMV launch's bytes (size_matched_read_us; pct_of_size_matched_read is their sum over the
+layer's time).
 
-Run: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--quick] [--section templates]
+Run: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--quick]
+                     [--section all|b1|templates|members|batched]
 """
 
 from __future__ import annotations
