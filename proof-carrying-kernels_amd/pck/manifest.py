@@ -38,6 +38,8 @@ LOCK_FORMAT = 2
 # Paths relative to PACKAGE_ROOT.
 TRUSTED = (
     "pck/fp.py",
+    "pck/checker.py",  # the CPU blocked checker
+    "pck/sampling.py",  # the CPU set-sampling checker
     "pck/member.py",
     "pck/vllm_plugin.py",  # builds every input to the in-vLLM membership verdicts
     "pck/cuda/checker.py",

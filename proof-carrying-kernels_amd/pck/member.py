@@ -9,15 +9,17 @@ For a row of logits ``l``, the sampled token ``t`` and the request's ``top_k`` /
   greedy  accept iff no logit is strictly larger than ``l[t]``;
   NaN logits or an id outside [0, V) reject.
 
-`check_members` runs the whole batch in one launch of the HIP kernel `pck_check_members`
-(exact FP32 comparisons, FP32 softmax terms on an exact split argument, FP64 sums); it needs
-the logits on the GPU.  `member_eps` / `member_eps32` are the error bounds the slack is built
-from (reference `src/pck/member.py:37-41,84-102`).
+`check_members` runs the whole batch in one launch of the HIP kernel (`pck_check_members_ex`:
+exact FP32 comparisons, FP32 softmax terms on an exact split argument, FP64 sums); it needs the
+logits on the GPU, and `launch_check` also keeps running totals on the device.  `check_member`
+is the reference's FP64 check of one row on the CPU.  `member_eps` / `member_eps32` are the
+error bounds the slack is built from (reference `src/pck/member.py:37-41,84-102`).
 """
 
 from __future__ import annotations
 
 import math
+from dataclasses import dataclass
 from typing import Any
 
 import numpy as np
@@ -29,6 +31,50 @@ def member_eps(vocab: int) -> float:
     """Error bound of the FP64 reference check: `pck.fp.softmax_eps` with the logits used
     directly (reference `src/pck/member.py:37-41`)."""
     return softmax_eps(vocab)
+
+
+@dataclass(frozen=True)
+class MemberVerdict:
+    """The verdict of `check_member` (reference `src/pck/member.py:45-50`)."""
+
+    ok: bool
+    above: int
+    """Logits strictly larger than the sampled token's (-1 for NaN logits or a bad id)."""
+    mass_above: float
+    """Fraction of the kept softmax mass strictly above the token (0 without top-p)."""
+
+
+def check_member(
+    logits: Any,
+    token: int,
+    top_k: int | None = None,
+    top_p: float | None = None,
+    *,
+    greedy: bool = False,
+    tol: float = 1e-4,
+) -> MemberVerdict:
+    """One row, in FP64 on the CPU (reference `src/pck/member.py:53-81`): NaN logits or an id
+    outside [0, V) reject; so does a token with k or more larger logits (k = 1 when greedy);
+    with top-p below 1 the kept set is every logit >= the k-th largest (all without top-k), r
+    is its softmax mass strictly above the token, and the row passes iff
+    r < next_up(top_p + next_up(tol + member_eps(V)))."""
+    row = np.asarray(logits, dtype=np.float64)
+    if np.isnan(row).any() or not 0 <= token < row.size:
+        return MemberVerdict(False, -1, math.nan)
+    lt = row[token]
+    above = int(np.count_nonzero(row > lt))
+    limit = 1 if greedy else top_k
+    if limit is not None and above >= limit:
+        return MemberVerdict(False, above, math.nan)
+    if greedy or top_p is None or top_p >= 1.0:
+        return MemberVerdict(True, above, 0.0)
+    kept = np.ones(row.size, dtype=bool)
+    if top_k is not None and top_k < row.size:
+        kept = row >= np.sort(row)[row.size - top_k]  # the k-th largest
+    terms = np.where(kept, np.exp(row - row[kept].max()), 0.0)
+    r = float(terms[row > lt].sum() / terms.sum())
+    slack = next_up(tol + member_eps(row.size))
+    return MemberVerdict(bool(r < next_up(top_p + slack)), above, r)
 
 
 def member_eps32(vocab: int) -> float:
