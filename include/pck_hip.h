@@ -76,6 +76,17 @@ struct PckCheckBatch;
 int pck_gemv_group_check(int weight_kind, const PckGemv* gemvs, int count, int threads,
                          const struct PckCheckBatch* ride, void* stream);
 
+/* FP8 grouped launch (optionally with carried checks, as pck_gemv_group_check) whose epilogue
+ * also dequantises: for item g, besides z = Q x in gemvs[g].y (the tree's exact bits, which the
+ * checker verifies against Q), it writes scaled[g][i] = scales[g][i] * z_i, one FP32 multiply
+ * rounded to nearest (the same bits as a separate y = s z).  scales[g] and scaled[g] are (m,)
+ * FP32 and must be non-null for every item with rows.  No reference counterpart: the reference
+ * applies the row scales of its quantizer (src/pck/cuda/gemv.py:41-58) in a separate op after
+ * gemv_fp8. */
+int pck_gemv_group_fp8_scaled(const PckGemv* gemvs, const float* const* scales,
+                              float* const* scaled, int count, int threads,
+                              const struct PckCheckBatch* ride, void* stream);
+
 /* Launch-shape knob of the coalesced kernels at threads = 256, for tuning sweeps: rows per wave
  * slot (1, 2 or 4), vector positions loaded ahead per lane (1, 2 or 4) and non-temporal weight
  * loads (0 or 1); rows_per_wave = 0 restores the built-in choice.  Changes only speed: outputs

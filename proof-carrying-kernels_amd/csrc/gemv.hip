@@ -50,7 +50,16 @@ struct GemvItem {
   int64_t m;
   int64_t n;
   int64_t per_lane;  // vectors per virtual lane: ceil(ceil(n / vec) / T)
+  const float* scale = nullptr;  // (m,) FP32 row scales of an FP8 weight, with y_scaled
+  float* y_scaled = nullptr;     // (m,) scale[i] * y[i], rounded to nearest; or null
 };
+
+// Writes row `row` of an item: the tree's sum, and the dequantised output when the item has
+// row scales (one FP32 multiply, as y = s z would round it).
+__device__ __forceinline__ void store_row(const GemvItem& it, int64_t row, float value) {
+  it.y[row] = value;
+  if (it.y_scaled != nullptr) it.y_scaled[row] = it.scale[row] * value;
+}
 
 struct GemvBatch {
   GemvItem item[PCK_MAX_GROUP];
@@ -314,7 +323,7 @@ __device__ __forceinline__ void gemv_rows(const GemvBatch& batch, int64_t group)
     const int64_t row = (wave * kSlots + slot) * R + r;
     if constexpr (kSlots == 2) {
       // T = 32: one virtual warp per row; lanes 0 and 32 hold the two rows' sums.
-      if (chain0 == 0 && live[r]) it.y[row] = acc[r][0];
+      if (chain0 == 0 && live[r]) store_row(it, row, acc[r][0]);
     } else {
       // Warp w = 2j + h is half h of chain slot j; reduce the T / 32 warp sums by halving.
       constexpr int kWarps = 2 * kChains;
@@ -328,7 +337,7 @@ __device__ __forceinline__ void gemv_rows(const GemvBatch& batch, int64_t group)
       for (int half = kWarps / 2; half > 0; half /= 2)
 #pragma unroll
         for (int i = 0; i < half; ++i) ws[i] = ws[i] + ws[i + half];
-      if (lane == 0 && live[r]) it.y[row] = ws[0];
+      if (lane == 0 && live[r]) store_row(it, row, ws[0]);
     }
   }
 }
@@ -537,7 +546,8 @@ struct GroupPlan {
 
 template <bool kFp8>
 hipError_t plan_group(const PckGemv* gemvs, double* const* sums, int count, int threads,
-                      GroupPlan& plan) {
+                      GroupPlan& plan, const float* const* scales = nullptr,
+                      float* const* scaled = nullptr) {
   constexpr int V = kFp8 ? 16 : 8;
   if (count < 1 || count > PCK_MAX_GROUP || gemvs == nullptr) return hipErrorInvalidValue;
   if (threads < kWarp || threads > 1024 || (threads & (threads - 1)) != 0)
@@ -554,6 +564,12 @@ hipError_t plan_group(const PckGemv* gemvs, double* const* sums, int count, int 
     const int64_t per_lane = ((n + V - 1) / V + threads - 1) / threads;
     plan.batch.item[g] =
         GemvItem{d.W, static_cast<const uint16_t*>(d.x), d.y, rs, d.m, n, per_lane};
+    if (scaled != nullptr && d.m > 0) {
+      if (scales == nullptr || scales[g] == nullptr || scaled[g] == nullptr)
+        return hipErrorInvalidValue;
+      plan.batch.item[g].scale = scales[g];
+      plan.batch.item[g].y_scaled = scaled[g];
+    }
     plan.rows += d.m;
     if (d.m > 0) {
       plan.vector = plan.vector && n % V == 0 && reinterpret_cast<uintptr_t>(d.W) % 16 == 0 &&
@@ -567,9 +583,10 @@ hipError_t plan_group(const PckGemv* gemvs, double* const* sums, int count, int 
 
 template <bool kFp8>
 hipError_t launch_group(const PckGemv* gemvs, int count, int threads, const PckCheckBatch* ride,
-                        hipStream_t stream) {
+                        hipStream_t stream, const float* const* scales = nullptr,
+                        float* const* scaled = nullptr) {
   GroupPlan plan;
-  if (plan_group<kFp8>(gemvs, nullptr, count, threads, plan) != hipSuccess)
+  if (plan_group<kFp8>(gemvs, nullptr, count, threads, plan, scales, scaled) != hipSuccess)
     return hipErrorInvalidValue;
   GemvBatch& batch = plan.batch;
   const bool vector = plan.vector, pad = plan.pad;
@@ -662,6 +679,14 @@ int pck_gemv_group_rowsums(int weight_kind, const PckGemv* gemvs, double* const*
 
 int pck_gemv_group(int weight_kind, const PckGemv* gemvs, int count, int threads, void* stream) {
   return pck_gemv_group_check(weight_kind, gemvs, count, threads, nullptr, stream);
+}
+
+int pck_gemv_group_fp8_scaled(const PckGemv* gemvs, const float* const* scales,
+                              float* const* scaled, int count, int threads,
+                              const PckCheckBatch* ride, void* stream) {
+  if (scales == nullptr || scaled == nullptr) return hipErrorInvalidValue;
+  return pck::launch_group<true>(gemvs, count, threads, ride, static_cast<hipStream_t>(stream),
+                                 scales, scaled);
 }
 
 int pck_gemv_bf16_naive(const void* W, const void* x, float* y, int64_t m, int64_t n, int threads,

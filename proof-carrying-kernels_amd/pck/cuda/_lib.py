@@ -142,6 +142,7 @@ SIGNATURES: dict[str, list[Any]] = {
     "pck_gemv_fp8_coalesced": [_p, _p, _p, _i64, _i64, _int, _p],
     "pck_gemv_group": [_int, ctypes.POINTER(PckGemv), _int, _int, _p],
     "pck_gemv_group_check": [_int, ctypes.POINTER(PckGemv), _int, _int, _p, _p],
+    "pck_gemv_group_fp8_scaled": [ctypes.POINTER(PckGemv), _p, _p, _int, _int, _p, _p],
     "pck_gemv_set_shape": [_int, _int, _int],
     "pck_bgemm": [_int, _p, _p, _p, _i64, _i64, _i64, _p],
     "pck_bgemm_set_shape": [_int, _int],

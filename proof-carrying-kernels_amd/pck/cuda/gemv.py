@@ -154,6 +154,59 @@ def gemv_group_check(
     return outs, results
 
 
+def gemv_group_fp8_scaled(
+    triples: Sequence[tuple[torch.Tensor, torch.Tensor, torch.Tensor]],
+    checks: Sequence[tuple[Any, torch.Tensor, torch.Tensor]] = (),
+    threads: int = 256,
+) -> tuple[list[torch.Tensor], list[torch.Tensor], list[Any]]:
+    """FP8 GEMVs that dequantise in the same launch: up to eight ``(Q, x, s)`` with Q E4M3FN
+    (m, n), x BF16 (n,) and s the (m,) FP32 row scales of `quantize_fp8`.  Returns
+    (z, y, check results): z = Q x with exactly the bits of `gemv_fp8` (what the checker
+    verifies against Q), y = s z rounded as ``s * z`` rounds it, and, as in
+    `gemv_group_check`, the results of ``checks`` carried in the launch.  No reference
+    counterpart: the reference scales in a separate op after `gemv_fp8`
+    (`src/pck/cuda/gemv.py:41-58`)."""
+    from pck.cuda.checker import batch_for
+
+    if not triples:
+        raise RuntimeError(f"group size must be in [1, {MAX_GROUP}], got 0")
+    pairs = [(Q, x) for Q, x, _ in triples]
+    if any(Q.dtype != torch.float8_e4m3fn for Q, _ in pairs):
+        raise RuntimeError("Q must be Float8_e4m3fn")
+    descs, outs, _, device = _group_descriptors(pairs, threads)
+    scales, scaled = [], []
+    for (Q, _, sc) in triples:
+        if not (sc.is_cuda and sc.device == device and sc.dtype == torch.float32 and sc.dim() == 1
+                and sc.size(0) == Q.size(0) and sc.is_contiguous()):  # fmt: skip
+            raise RuntimeError(f"s must be a contiguous ({Q.size(0)},) float32 tensor on {device}")
+        scales.append(sc)
+        scaled.append(torch.empty(Q.size(0), dtype=torch.float32, device=device))
+    s_ptrs = (ctypes.c_void_p * len(triples))(*[t.data_ptr() for t in scales])
+    y_ptrs = (ctypes.c_void_p * len(triples))(*[t.data_ptr() for t in scaled])
+    ride = None
+    results: list[Any] = []
+    if checks:
+        ride, results, check_device = batch_for(checks)
+        if check_device != device:
+            raise RuntimeError("the checks must be on the GEMVs' device")
+    with torch.cuda.device(device):
+        err = lib().pck_gemv_group_fp8_scaled(
+            descs, s_ptrs, y_ptrs, len(triples), threads,
+            None if ride is None else ctypes.byref(ride), stream_handle(device),
+        )  # fmt: skip
+    check(err, "grouped fp8 gemv launch")
+    return outs, scaled, results
+
+
+def gemv_fp8_scaled(
+    Q: torch.Tensor, x: torch.Tensor, s: torch.Tensor, threads: int = 256
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """(z, y) for one FP8 GEMV: z = Q x (the bits of `gemv_fp8`) and y = s z dequantised in the
+    same launch."""
+    z, y, _ = gemv_group_fp8_scaled([(Q, x, s)], (), threads)
+    return z[0], y[0]
+
+
 def gemv_group(
     pairs: Sequence[tuple[torch.Tensor, torch.Tensor]], threads: int = 256
 ) -> list[torch.Tensor]:

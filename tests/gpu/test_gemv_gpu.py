@@ -347,6 +347,51 @@ def test_quantize_fp8_codes_are_the_nearest_e4m3() -> None:
     assert (v[0] != 0).sum() > 1000 and len(np.unique(got[0])) == 254
 
 
+@pytest.mark.parametrize(("m", "n"), [(4096, 4096), (4096, 14336), (37, 1000)])
+def test_fp8_scaled_epilogue(m: int, n: int) -> None:
+    """The dequantising launch writes z with exactly gemv_fp8's bits and y = s z with exactly
+    the bits of torch's s * z (one FP32 multiply), on the vector path and on the element path
+    (n = 1000 is not a multiple of 16)."""
+    from pck.cuda import gemv_fp8_scaled
+
+    g = torch.Generator().manual_seed(m + n)
+    W = (torch.randn(m, n, generator=g) * 0.02).to(torch.bfloat16).cuda()
+    x = torch.randn(n, generator=g).to(torch.bfloat16).cuda()
+    Q, s = quantize_fp8(W)
+    z, y = gemv_fp8_scaled(Q, x, s)
+    assert torch.equal(z.view(torch.int32), gemv_fp8(Q, x).view(torch.int32))
+    assert torch.equal(y.view(torch.int32), (s * z).view(torch.int32))
+
+
+def test_fp8_scaled_group_carries_checks() -> None:
+    """q, k, v in one dequantising launch that also carries the checks of earlier outputs:
+    every z and y as in single launches, and the check results bit-identical to check_many."""
+    from pck.cuda import GpuBlockedChecker, check_many, gemv_group_fp8_scaled
+
+    g = torch.Generator().manual_seed(2)
+    shapes = [(4096, 4096), (1024, 4096), (1024, 4096)]
+    triples, checks = [], []
+    for m, n in shapes:
+        W = (torch.randn(m, n, generator=g) * 0.02).to(torch.bfloat16).cuda()
+        Q, s = quantize_fp8(W)
+        x = torch.randn(n, generator=g).to(torch.bfloat16).cuda()
+        triples.append((Q, x, s))
+        checker = GpuBlockedChecker(Q.to(torch.bfloat16), 128, tree_height(n, 256, 16),
+                                    generator=torch.Generator().manual_seed(m))  # fmt: skip
+        checks.append((checker, x, gemv_fp8(Q, x)))
+    zs, ys, results = gemv_group_fp8_scaled(triples, checks)
+    want = check_many(checks)
+    for (Q, x, s), z, y in zip(triples, zs, ys, strict=True):
+        assert torch.equal(z.view(torch.int32), gemv_fp8(Q, x).view(torch.int32))
+        assert torch.equal(y.view(torch.int32), (s * z).view(torch.int32))
+    for got, ref in zip(results, want, strict=True):
+        assert torch.equal(got.passed, ref.passed) and bool(got.passed.all())
+        assert torch.equal(got.rho.view(torch.int64), ref.rho.view(torch.int64))
+        assert torch.equal(got.tau.view(torch.int64), ref.tau.view(torch.int64))
+    with pytest.raises(RuntimeError, match="float32"):
+        gemv_group_fp8_scaled([(triples[0][0], triples[0][1], triples[0][2].double())])
+
+
 def test_fp8_rejects_bf16_weights() -> None:
     W, x = fp8_problem(4, 32, seed=0)
     with pytest.raises(RuntimeError, match="Float8_e4m3fn"):
