@@ -97,8 +97,9 @@ BLOCKS = (128, 256)  # checker block sizes measured (rows per checksum)
 
 
 def build_layers(copies: int, fp8: bool, gen):  # type: ignore[no-untyped-def]
-    """``copies`` layer copies; layer[name] = {"W", "x", "bank": {b: GpuBlockedChecker},
-    "rows": {b: RowSumChecker}} for each projection and checker block b."""
+    """``copies`` layer copies; layer[name] = {"W", "x", "s", "bank": {b: GpuBlockedChecker},
+    "rows": {b: RowSumChecker}} for each projection and checker block b (FP8: W holds the
+    E4M3 codes Q and s the row scales of `quantize_fp8`; BF16: s is None)."""
     import torch
 
     from pck.cuda import GpuBlockedChecker, RowSumChecker, quantize_fp8
@@ -111,13 +112,15 @@ def build_layers(copies: int, fp8: bool, gen):  # type: ignore[no-untyped-def]
         for name, m, n in LAYER:
             W = (torch.randn(m, n, generator=gen) * 0.02).to(torch.bfloat16).cuda()
             x = torch.randn(n, generator=gen).to(torch.bfloat16).cuda()
+            s = None
             if fp8:
-                W = quantize_fp8(W)[0]
+                W, s = quantize_fp8(W)
             h = tree_height(n, THREADS, vec)
             checked = W.to(torch.bfloat16) if fp8 else W  # FP8: the bound is on Q itself
             layer[name] = {
                 "W": W,
                 "x": x,
+                "s": s,
                 "bank": {b: GpuBlockedChecker(checked, b, h, generator=gen) for b in BLOCKS},
                 "rows": {b: RowSumChecker(m, n, b, h, generator=gen) for b in BLOCKS},
             }
@@ -169,6 +172,11 @@ def run_step(layer, with_check: bool, events=None):  # type: ignore[no-untyped-d
 # (the cost of the sums alone).  A _b256 suffix: checker block b = 256 instead of 128.
 MODES = ("gemv", "serial", "side_stream", "carried", "carried_b256", "inpass", "inpass_b256",
          "inpass_sums")  # fmt: skip
+# FP8 only, with the row scales applied (y = s z).  gemv_scale_after: the GEMVs, then one
+# elementwise multiply per output (the reference's order).  gemv_scaled: the GEMVs with the
+# multiply in their epilogue (pck_gemv_group_fp8_scaled).  carried_scaled: the carried checks
+# riding in the scaled launches.
+FP8_MODES = MODES + ("gemv_scale_after", "gemv_scaled", "carried_scaled")
 
 # In the carried and in-pass modes the gate_up launch of layer L also checks every output
 # finished since the previous gate_up: the previous layer's gate, up and down and this layer's
@@ -188,11 +196,14 @@ CARRIES = {
 LAST_CHECKED = ("gate", "up", "down")  # the pass's final standalone check
 
 
-def carried_pass(layers, depth: int, block: int, inpass: bool, checks: bool = True):  # type: ignore[no-untyped-def]
+def carried_pass(layers, depth: int, block: int, inpass: bool, checks: bool = True,  # type: ignore[no-untyped-def]
+                 scaled: bool = False):  # fmt: skip
     """One decode pass of ``depth`` layers whose checks ride in later launches: bank checks
-    (pck_gemv_group_check) or, with ``inpass``, row-sum checks of in-pass GEMVs
+    (pck_gemv_group_check; with ``scaled``, FP8 launches that also write y = s z,
+    pck_gemv_group_fp8_scaled) or, with ``inpass``, row-sum checks of in-pass GEMVs
     (pck_gemv_group_rowsums).  Returns every check result."""
-    from pck.cuda import check_many, gemv_group_check, gemv_group_rowsums, rowsum_check_many
+    from pck.cuda import (check_many, gemv_group_check, gemv_group_fp8_scaled, gemv_group_rowsums,
+                          rowsum_check_many)  # fmt: skip
 
     results = []
     prev = None  # (layer, outputs, sums) of the previous layer
@@ -212,6 +223,9 @@ def carried_pass(layers, depth: int, block: int, inpass: bool, checks: bool = Tr
             if inpass:
                 ys, ss, res = gemv_group_rowsums(pairs(layer, names), items, THREADS)
                 sums.update(zip(names, ss))
+            elif scaled:
+                triples = [(layer[n]["W"], layer[n]["x"], layer[n]["s"]) for n in names]
+                ys, _, res = gemv_group_fp8_scaled(triples, items, THREADS)
             else:
                 ys, res = gemv_group_check(pairs(layer, names), items, THREADS)
             results.extend(res)
@@ -230,17 +244,29 @@ def carried_pass(layers, depth: int, block: int, inpass: bool, checks: bool = Tr
 
 def capture(layers, mode: str, depth: int):  # type: ignore[no-untyped-def]
     """One HIP graph holding a decode pass of ``depth`` layers (cycling over the layer copies)
-    in ``mode`` (see MODES).  Only this library's kernels are captured (no memset, no library
-    reduction).  Returns (graph, the pass's check results and outputs)."""
+    in ``mode`` (see MODES and FP8_MODES).  Only this library's kernels are captured, and in
+    gemv_scale_after torch's elementwise multiply (no memset, no library reduction).  Returns (graph, the pass's check results and outputs)."""
     import torch
 
-    from pck.cuda import check_many
+    from pck.cuda import check_many, gemv_group, gemv_group_fp8_scaled
 
     def body():  # type: ignore[no-untyped-def]
         if mode.startswith(("carried", "inpass")):
             block = 256 if mode.endswith("_b256") else BLOCK
-            return carried_pass(layers, depth, block, mode.startswith("inpass"), mode != "inpass_sums")
+            return carried_pass(layers, depth, block, mode.startswith("inpass"), mode != "inpass_sums",
+                                mode == "carried_scaled")  # fmt: skip
         keep = []
+        if mode in ("gemv_scale_after", "gemv_scaled"):
+            for i in range(depth):
+                layer = layers[i % len(layers)]
+                for _, names in LAUNCHES:
+                    if mode == "gemv_scaled":
+                        triples = [(layer[n]["W"], layer[n]["x"], layer[n]["s"]) for n in names]
+                        keep.extend(gemv_group_fp8_scaled(triples, (), THREADS)[1])
+                    else:
+                        zs = gemv_group(pairs(layer, names), THREADS)
+                        keep.extend(torch.mul(layer[n]["s"], z) for n, z in zip(names, zs))
+            return keep
         cap = torch.cuda.current_stream()
         for i in range(depth):
             layer = layers[i % len(layers)]
@@ -306,14 +332,15 @@ def honest_verdicts(keep) -> tuple[int, int]:  # type: ignore[no-untyped-def]
     return checked, rejected
 
 
-def b1_modes(layers, depth: int, rounds: int) -> tuple[dict, dict]:  # type: ignore[no-untyped-def]
-    """ms per layer of every mode (alternating rounds) and the honest-run verdict counts."""
-    captured = {mode: capture(layers, mode, depth) for mode in MODES}
+def b1_modes(layers, depth: int, rounds: int, modes=MODES) -> tuple[dict, dict]:  # type: ignore[no-untyped-def]
+    """ms per layer of every mode in ``modes`` (alternating rounds) and the honest-run verdict
+    counts."""
+    captured = {mode: capture(layers, mode, depth) for mode in modes}
     ms = timed_modes({mode: graph for mode, (graph, _) in captured.items()}, depth, rounds)
     verdicts = {}
     for mode, (_, keep) in captured.items():
         checked, rejected = honest_verdicts(keep)
-        expect = 0 if mode in ("gemv", "inpass_sums") else 7 * depth
+        expect = 0 if mode.startswith("gemv") or mode == "inpass_sums" else 7 * depth
         n_results = sum(1 for r in keep if hasattr(r, "passed"))
         assert n_results == expect, (mode, n_results)
         assert rejected == 0, f"{mode}: the checker rejected {rejected} honest blocks"
@@ -1055,8 +1082,9 @@ def b1_section(fp8: bool, copies: int, depth: int, rounds: int, quick: bool, ste
     print(f"[bench] building {copies} {kind} layer copies", file=sys.stderr, flush=True)
     layers = build_layers(copies, fp8, gen)
     nbytes = sum(gemv_bytes(m, n, 1 if fp8 else 2) for _, m, n in LAYER)
-    print(f"[bench] timing {kind} passes ({len(MODES)} modes, {rounds} rounds)", file=sys.stderr, flush=True)
-    ms, checked = b1_modes(layers, depth, rounds)
+    modes = FP8_MODES if fp8 else MODES
+    print(f"[bench] timing {kind} passes ({len(modes)} modes, {rounds} rounds)", file=sys.stderr, flush=True)
+    ms, checked = b1_modes(layers, depth, rounds, modes)
     base = ms["gemv"]
     out: dict = {
         "gemv_only_gbps": round(nbytes / (base / 1e3) / 1e9, 1),
@@ -1206,6 +1234,8 @@ def main() -> None:
             "gemv_only_gbps": b8["gemv_only_gbps"],
             "ms_per_step": b8["modes_ms"]["carried"],
             "pct_of_size_matched_read": round(100 * sum(matched[1].values()) / b8["modes_ms"]["carried"], 2),
+            # y = s z: a separate multiply after the GEMVs against the multiply in their epilogue
+            "dequant_ms": {k: b8["modes_ms"][k] for k in ("gemv_scale_after", "gemv_scaled", "carried_scaled")},
         },
         "checker_overhead_pct": ovh(b16),
         "fp8_checker_overhead_pct": ovh(b8),

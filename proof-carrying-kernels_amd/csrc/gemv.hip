@@ -54,11 +54,12 @@ struct GemvItem {
   float* y_scaled = nullptr;     // (m,) scale[i] * y[i], rounded to nearest; or null
 };
 
-// Writes row `row` of an item: the tree's sum, and the dequantised output when the item has
-// row scales (one FP32 multiply, as y = s z would round it).
-__device__ __forceinline__ void store_row(const GemvItem& it, int64_t row, float value) {
+// Writes row `row` of an item: the tree's sum, and the dequantised output `scale * value` when
+// the item has row scales (one FP32 multiply, as y = s z would round it).
+__device__ __forceinline__ void store_row(const GemvItem& it, int64_t row, float value,
+                                          float scale) {
   it.y[row] = value;
-  if (it.y_scaled != nullptr) it.y_scaled[row] = it.scale[row] * value;
+  if (it.y_scaled != nullptr) it.y_scaled[row] = scale * value;
 }
 
 struct GemvBatch {
@@ -232,6 +233,15 @@ __device__ __forceinline__ void gemv_rows(const GemvBatch& batch, int64_t group)
         static_cast<const unsigned char*>(it.W) + (live[r] ? row : it.m - 1) * n * kElemBytes;
   }
 
+  // Row scales of a scaled FP8 item, loaded ahead of the weight stream so that their latency
+  // is hidden behind it instead of adding a dependent load to the launch's tail.
+  float scale[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t row = (wave * kSlots + slot) * R + r;
+    scale[r] = (kFp8 && it.y_scaled != nullptr) ? it.scale[live[r] ? row : it.m - 1] : 1.0f;
+  }
+
   float acc[R][kChains];
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -323,7 +333,7 @@ __device__ __forceinline__ void gemv_rows(const GemvBatch& batch, int64_t group)
     const int64_t row = (wave * kSlots + slot) * R + r;
     if constexpr (kSlots == 2) {
       // T = 32: one virtual warp per row; lanes 0 and 32 hold the two rows' sums.
-      if (chain0 == 0 && live[r]) store_row(it, row, acc[r][0]);
+      if (chain0 == 0 && live[r]) store_row(it, row, acc[r][0], scale[r]);
     } else {
       // Warp w = 2j + h is half h of chain slot j; reduce the T / 32 warp sums by halving.
       constexpr int kWarps = 2 * kChains;
@@ -337,7 +347,7 @@ __device__ __forceinline__ void gemv_rows(const GemvBatch& batch, int64_t group)
       for (int half = kWarps / 2; half > 0; half /= 2)
 #pragma unroll
         for (int i = 0; i < half; ++i) ws[i] = ws[i] + ws[i + half];
-      if (lane == 0 && live[r]) store_row(it, row, ws[0]);
+      if (lane == 0 && live[r]) store_row(it, row, ws[0], scale[r]);
     }
   }
 }
