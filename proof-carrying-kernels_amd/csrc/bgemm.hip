@@ -30,9 +30,11 @@
 // tiles of 32); wave w owns K segment w for all of them, so each MFMA tile of the workgroup is
 // summed by eight waves and the eight segment sums meet in LDS in the tree order above.
 //   Packed kernel (pck_bgemm_packed): weights and activations in the 32-row tile layout below,
-//   so each load feeds two K-steps of one MFMA operand; rolling register rings keep 16 (8 at
-//   four tiles) K-steps of both operands in flight per lane; the batch passes of one row tile are
-//   dispatched to the same XCD (workgroup g runs on XCD g % 8), so their repeated weight reads
+//   so each load feeds two K-steps of one MFMA operand; rolling register rings keep 8 (4 at
+//   four tiles) K-steps of both operands in flight per lane; a workgroup takes R weight tiles
+//   by T batch tiles at a time and, where a CU holds one workgroup, loops over such items with
+//   the next item's first operands loaded during the current one's last steps; the batch
+//   passes of one row group run at the same time on one XCD, so their repeated weight reads
 //   are served by that XCD's L2.
 //   Element kernel (pck_bgemm: any n, any alignment, row-major operands): the same order with
 //   element loads, one K-step at a time.
@@ -41,7 +43,10 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+#include <climits>
 #include <cstdint>
+#include <type_traits>
 #include <utility>
 
 #include "pck_hip.h"
@@ -239,7 +244,6 @@ __global__ void __launch_bounds__(kThreads) bgemm_kernel(BgemmArgs a) {
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr uint32_t kOutOfRange = 0x80000000u;  // a lane offset past every buffer (reads 0)
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
@@ -283,13 +287,20 @@ struct PackedArgs {
   int64_t passes;
 };
 
-// R row tiles (32 weight rows each) and T batch tiles per workgroup: every wave multiplies its
-// K segment of R weight tiles by the same T batch tiles, so each batch load serves R tiles.
+// R row tiles (32 weight rows each) and T batch tiles per item: every wave multiplies its K
+// segment of R weight tiles by the same T batch tiles, so each batch load serves R tiles.
 template <int R, int T>
 constexpr int ring_pairs() {
-  return R + T >= 4 ? 4 : 8;
+  return R + T >= 4 ? 2 : 4;
 }
 
+// An item is one (row group, batch pass): R row tiles by T batch tiles.  The grid holds as
+// many workgroups as the GPU keeps resident, and workgroup w takes items w, w + G, w + 2 G, ...
+// (G workgroups).  During an item's last ring pass the refills already fetch the next item's
+// first step pairs, so only a workgroup's first item waits a full memory latency before its
+// first step.  Item g -> (row group, pass): with the groups a multiple of 8, the passes of a
+// row group are items 8 apart, which run at about the same time on one XCD (workgroup w runs
+// on XCD w % 8 when G is a multiple of 8), so their repeated weight reads hit that XCD's L2.
 template <int R, int T, bool kFp8>
 __global__ void __launch_bounds__(kThreads) bgemm_packed_kernel(PackedArgs a) {
   constexpr uint32_t kQ = kFp8 ? 8 : 16;  // weight bytes per lane and step pair
@@ -304,61 +315,73 @@ __global__ void __launch_bounds__(kThreads) bgemm_packed_kernel(PackedArgs a) {
   const int l = lane & 31;
   const int h = lane >> 5;
 
-  // Workgroup -> (row group, batch pass); the passes of a row group share an XCD.
-  const int64_t g = blockIdx.x;
   const int64_t groups = (a.row_tiles + R - 1) / R;
-  int64_t rg, bp;
-  if (a.passes > 1 && groups % 8 == 0) {
-    const int64_t xcd = g % 8, local = g / 8;
-    rg = (local / a.passes) * 8 + xcd;
-    bp = local % a.passes;
-  } else {
-    rg = g / a.passes;
-    bp = g % a.passes;
-  }
-  const int64_t rt0 = rg * R;
-  const int64_t rows_here = a.row_tiles - rt0 < R ? a.row_tiles - rt0 : R;
+  const int64_t items = groups * a.passes;
   // Segments of whole step pairs (the host requires n % 128 == 0, so per is even).
   const int64_t chunks = a.n / kStep;
   const int64_t per = (chunks + kWaves - 1) / kWaves;
   const int64_t c_lo = wave * per < chunks ? wave * per : chunks;
   const int64_t c_hi = c_lo + per < chunks ? c_lo + per : chunks;
   const int pairs = static_cast<int>(c_hi - c_lo) / 2;
+  const int last = pairs - 1;
 
-  // One buffer per operand: this row group of the weights, this pass's batch tiles.
+  // One buffer per operand and item: the item's row group of the weights and its pass's batch
+  // tiles.  Tiles past the end (a partial last group or pass) lie past the buffer and read 0.
   const uint32_t w_tile_bytes = static_cast<uint32_t>(chunks / 2 * 64 * kQ);
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.Wp + rt0 * w_tile_bytes,
-                                              static_cast<uint32_t>(rows_here) * w_tile_bytes);
-  const int64_t t0 = bp * T;
-  const int64_t tiles_here = a.batch_tiles - t0 < T ? a.batch_tiles - t0 : T;
   const uint32_t x_tile_bytes = static_cast<uint32_t>(chunks / 2 * 64 * 16);
-  const __amdgpu_buffer_rsrc_t rx =
-      make_rsrc(a.Xp + t0 * x_tile_bytes, static_cast<uint32_t>(tiles_here) * x_tile_bytes);
+  struct Item {
+    const char* w_base;  // the row group's first tile
+    const char* x_base;  // the pass's first batch tile
+    uint32_t w_bytes, x_bytes;
+    int64_t rt0, t0;
+  };
+  // 32-bit index arithmetic (the host keeps items below 2^31).
+  const uint32_t passes = static_cast<uint32_t>(a.passes);
+  const bool by_xcd = passes > 1 && groups % 8 == 0;
+  auto item_at = [&](int64_t g64) {
+    const uint32_t g = static_cast<uint32_t>(g64);
+    uint32_t rg, bp;
+    if (by_xcd) {
+      const uint32_t xcd = g % 8, local = g / 8;
+      rg = (local / passes) * 8 + xcd;
+      bp = local % passes;
+    } else {
+      rg = g / passes;
+      bp = g % passes;
+    }
+    Item it;
+    it.rt0 = static_cast<int64_t>(rg) * R;
+    const int64_t rows_here = a.row_tiles - it.rt0 < R ? a.row_tiles - it.rt0 : R;
+    it.w_base = a.Wp + it.rt0 * w_tile_bytes;
+    it.w_bytes = static_cast<uint32_t>(rows_here) * w_tile_bytes;
+    it.t0 = static_cast<int64_t>(bp) * T;
+    const int64_t tiles_here = a.batch_tiles - it.t0 < T ? a.batch_tiles - it.t0 : T;
+    it.x_base = a.Xp + it.t0 * x_tile_bytes;
+    it.x_bytes = static_cast<uint32_t>(tiles_here) * x_tile_bytes;
+    return it;
+  };
   uint32_t w_voff[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    w_voff[r] = r < rows_here
-                    ? static_cast<uint32_t>(r * w_tile_bytes + (c_lo / 2 * 64 + lane) * kQ)
-                    : kOutOfRange;
-  }
+  for (int r = 0; r < R; ++r) w_voff[r] = static_cast<uint32_t>(r * w_tile_bytes + (c_lo / 2 * 64 + lane) * kQ);
   uint32_t x_voff[T];
 #pragma unroll
-  for (int t = 0; t < T; ++t) {
-    x_voff[t] = t < tiles_here
-                    ? static_cast<uint32_t>(t * x_tile_bytes + (c_lo / 2 * 64 + lane) * 16)
-                    : kOutOfRange;
-  }
+  for (int t = 0; t < T; ++t) x_voff[t] = static_cast<uint32_t>(t * x_tile_bytes + (c_lo / 2 * 64 + lane) * 16);
   constexpr uint32_t kWs = 64 * kQ;  // weight bytes per step pair
   constexpr uint32_t kXs = 64 * 16;  // batch bytes per step pair and tile
 
+  auto load_w = [&](__amdgpu_buffer_rsrc_t rw, int r, int pair) {
+    if constexpr (kFp8) return load8(rw, w_voff[r], pair * kWs);
+    else return load16(rw, w_voff[r], pair * kWs);
+  };
+  auto load_x = [&](__amdgpu_buffer_rsrc_t rx, int t, int pair) {
+    return load16(rx, x_voff[t], pair * kXs);
+  };
+
   f32x16 acc[R][T], grp[R][T];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int t = 0; t < T; ++t)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[r][t][v] = grp[r][t][v] = -0.0f;
-  // A group of kGroup chunks is kGroup / 2 step pairs; its sum joins the wave sum.
+  const f32x16 zero16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f,
+                         0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  // A group of kGroup chunks is kGroup / 2 step pairs, summed from -0.0; its sum joins the wave
+  // sum.  -0.0 + d is d for every d, so a group's first step assigns its products instead.
   constexpr int kGroupPairs = kGroup / 2;
   static_assert(kGroupPairs % ring_pairs<R, T>() == 0, "groups end at ring pass ends");
   auto flush = [&]() {
@@ -367,130 +390,192 @@ __global__ void __launch_bounds__(kThreads) bgemm_packed_kernel(PackedArgs a) {
 #pragma unroll
       for (int t = 0; t < T; ++t)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          acc[r][t][v] = acc[r][t][v] + grp[r][t][v];
-          grp[r][t][v] = -0.0f;
-        }
-  };
-  const f32x16 zero16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f,
-                         0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-
-  auto load_w = [&](int r, int pair) {
-    if constexpr (kFp8) return load8(rw, w_voff[r], pair * kWs);
-    else return load16(rw, w_voff[r], pair * kWs);
+        for (int v = 0; v < 16; ++v) acc[r][t][v] = acc[r][t][v] + grp[r][t][v];
   };
 
   // Rolling register rings: pair q uses slot q % kRing, which is refilled with pair q + kRing
-  // as soon as it is used.  Refills past the segment reload its last pair (unused), so every
-  // load is unconditional and the loads in flight are counted exactly.
+  // as soon as it is used: from this item while it has one, else from the next item (pair
+  // q + kRing - pairs, in the same slot when pairs % kRing == 0), else the item's last pair
+  // again (unused), so every load is unconditional and the loads in flight are counted exactly.
   u32x4 w[kRing][R];
   u32x4 x[kRing][T];
-  const int last = pairs - 1;
-  if (pairs > 0) {
+  auto fill = [&](const Item& it) {
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(it.w_base, it.w_bytes);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(it.x_base, it.x_bytes);
 #pragma unroll
     for (int k = 0; k < kRing; ++k) {
       const int q = k < last ? k : last;
 #pragma unroll
-      for (int r = 0; r < R; ++r) w[k][r] = load_w(r, q);
+      for (int r = 0; r < R; ++r) w[k][r] = load_w(rw, r, q);
 #pragma unroll
-      for (int t = 0; t < T; ++t) x[k][t] = load16(rx, x_voff[t], q * kXs);
+      for (int t = 0; t < T; ++t) x[k][t] = load_x(rx, t, q);
     }
-  }
-  // Pair q with ring slot k: two steps of one MFMA per batch tile and 16 adds each, in step
-  // order, then the slot's refill.
-  auto pair_step = [&](int q, auto k_const) {
-    constexpr int k = decltype(k_const)::value;
+  };
+
+  // n % 128 == 0 (checked on the host) gives every wave per = n / 64 chunks, so pairs >= 1
+  // and is the same in every wave.
+  int64_t g = blockIdx.x;
+  if (g >= items) return;  // uniform
+  Item cur = item_at(g);
+  fill(cur);
+  for (;;) {
+    const int64_t g_next = g + gridDim.x;
+    const bool has_next = g_next < items;  // uniform
+    const bool chain = has_next && pairs % kRing == 0;
+    const Item nxt = has_next ? item_at(g_next) : cur;
+
+    // The refill source of one ring pass (pairs base .. base + kRing - 1): the pass whose
+    // refills run past this item's last pair takes them from the next item when chaining.
+    struct Refill {
+      __amdgpu_buffer_rsrc_t rw, rx;
+      bool next;
+    };
+    auto refill_for = [&](int base) {
+      const bool next = chain && base + kRing > last;  // uniform
+      return Refill{make_rsrc(next ? nxt.w_base : cur.w_base, next ? nxt.w_bytes : cur.w_bytes),
+                    make_rsrc(next ? nxt.x_base : cur.x_base, next ? nxt.x_bytes : cur.x_bytes),
+                    next};
+    };
+    // Pair q with ring slot k: two steps of one MFMA per (row tile, batch tile), each step's
+    // products added to its group sum (kFirst: the group's first step, assigned), then the
+    // slot's refill.
+    auto pair_step = [&](int q, auto k_const, auto first_const, const Refill& rf) {
+      constexpr int k = decltype(k_const)::value;
+      constexpr bool kFirst = decltype(first_const)::value;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const s16x4 wv = w_step<kFp8>(w[k][r], j);
+#pragma unroll
+          for (int t = 0; t < T; ++t) {
+            const f32x16 d = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(wv, x_step(x[k][t], j),
+                                                                     zero16, 0, 0, 0);
+            if (kFirst && j == 0) {
+              grp[r][t] = d;
+            } else {
+#pragma unroll
+              for (int v = 0; v < 16; ++v) grp[r][t][v] = grp[r][t][v] + d[v];
+            }
+          }
+        }
+      }
+      const int qn = q + kRing;
+      const int pn = rf.next ? qn - pairs : (qn < last ? qn : last);
+#pragma unroll
+      for (int r = 0; r < R; ++r) w[k][r] = load_w(rf.rw, r, pn);
+#pragma unroll
+      for (int t = 0; t < T; ++t) x[k][t] = load_x(rf.rx, t, pn);
+    };
+    using No = std::false_type;
+
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[r][t][v] = -0.0f;
+    // Whole groups: ring passes with no exit inside, so the loads in flight are the same on
+    // every entry to the loop head and no step waits for more than its own operands.
+    const int whole = pairs / kGroupPairs * kGroupPairs;
+    for (int base = 0; base < whole; base += kGroupPairs) {
+      auto ring_pass = [&](auto p_const) {
+        constexpr int P = decltype(p_const)::value;
+        const Refill rf = refill_for(base + P * kRing);
+        [&]<int... K>(std::integer_sequence<int, K...>) {
+          (pair_step(base + P * kRing + K, std::integral_constant<int, K>{},
+                     std::integral_constant<bool, P == 0 && K == 0>{}, rf), ...);
+        }(std::make_integer_sequence<int, kRing>{});
+      };
+      [&]<int... P>(std::integer_sequence<int, P...>) {
+        (ring_pass(std::integral_constant<int, P>{}), ...);
+      }(std::make_integer_sequence<int, kGroupPairs / kRing>{});
+      flush();
+    }
+    // The last group, shorter than kGroupPairs: whole ring passes, then a partial one.
+    if (whole < pairs) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) grp[r][t][v] = -0.0f;
+      const int full = pairs / kRing * kRing;
+      for (int base = whole; base < full; base += kRing) {
+        const Refill rf = refill_for(base);
+        [&]<int... K>(std::integer_sequence<int, K...>) {
+          (pair_step(base + K, std::integral_constant<int, K>{}, No{}, rf), ...);
+        }(std::make_integer_sequence<int, kRing>{});
+      }
+      const Refill rf = refill_for(full);  // chaining implies full == pairs: no pair runs here
+      [&]<int... K>(std::integer_sequence<int, K...>) {
+        ((full + K < pairs ? (pair_step(full + K, std::integral_constant<int, K>{}, No{}, rf), 0) : 0), ...);
+      }(std::make_integer_sequence<int, kRing>{});
+      flush();
+    }
+
+    // Segment sums meet in LDS, one row tile at a time:
+    // ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7)).
+    __shared__ float red[4][T][16][64];
+    // r is a compile-time index (a fold over 0 .. R - 1), so acc stays in registers.
+    auto reduce_tile = [&](auto r_const) {
+      constexpr int r = decltype(r_const)::value;
+      auto put = [&](int slot) {
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) red[slot][t][v][lane] = acc[r][t][v];
+      };
+      auto take = [&](int slot) {
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[r][t][v] = acc[r][t][v] + red[slot][t][v][lane];
+      };
+      __syncthreads();  // the previous tile's (or item's) last reads of the slots
+      if (wave & 1) put(wave / 2);
+      __syncthreads();
+      if (!(wave & 1)) take(wave / 2);  // waves 0, 2, 4, 6 hold s01, s23, s45, s67
+      if (wave == 2) put(1);
+      if (wave == 6) put(3);
+      __syncthreads();
+      if (wave == 0) take(1);  // s0123
+      if (wave == 4) take(3);  // s4567
+      if (wave == 4) put(2);
+      __syncthreads();
+      if (wave == 0) take(2);
+    };
+    [&]<int... Rs>(std::integer_sequence<int, Rs...>) {
+      (reduce_tile(std::integral_constant<int, Rs>{}), ...);
+    }(std::make_integer_sequence<int, R>{});
+
+    // MFMA output layout: D[i][b] sits in lane b + 32 ((i / 4) % 2), register 4 (i / 8) + i % 4,
+    // so registers 4q .. 4q + 3 of a lane are four consecutive weight rows of one batch row.
+    if (wave == 0) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const s16x4 wv = w_step<kFp8>(w[k][r], j);
+        const int64_t rt = cur.rt0 + r;
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-          const f32x16 d = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(wv, x_step(x[k][t], j),
-                                                                   zero16, 0, 0, 0);
+          const int64_t b = (cur.t0 + t) * 32 + l;
+          if (b >= a.batch) continue;
+          float* yrow = a.Y + b * a.m + rt * kRows + 4 * h;
 #pragma unroll
-          for (int v = 0; v < 16; ++v) grp[r][t][v] = grp[r][t][v] + d[v];
+          for (int q = 0; q < 4; ++q) {
+            const int64_t i = rt * kRows + 8 * q + 4 * h;
+            if (i < a.m) {
+              *reinterpret_cast<float4*>(yrow + 8 * q) =
+                  make_float4(acc[r][t][4 * q], acc[r][t][4 * q + 1], acc[r][t][4 * q + 2],
+                              acc[r][t][4 * q + 3]);
+            }
+          }
         }
       }
     }
-    const int qn = q + kRing < last ? q + kRing : last;
-#pragma unroll
-    for (int r = 0; r < R; ++r) w[k][r] = load_w(r, qn);
-#pragma unroll
-    for (int t = 0; t < T; ++t) x[k][t] = load16(rx, x_voff[t], qn * kXs);
-  };
-  // Whole ring passes have no exit inside, so the loads in flight are the same on every entry
-  // to the loop head and no step waits for more than its own operands.
-  const int full = pairs / kRing * kRing;
-  for (int base = 0; base < full; base += kRing) {
-    [&]<int... K>(std::integer_sequence<int, K...>) {
-      (pair_step(base + K, std::integral_constant<int, K>{}), ...);
-    }(std::make_integer_sequence<int, kRing>{});
-    if ((base + kRing) % kGroupPairs == 0) flush();  // uniform
-  }
-  // The last partial pass (segments that are not a whole number of passes); it stays inside
-  // one group, which ends with the segment.
-  [&]<int... K>(std::integer_sequence<int, K...>) {
-    ((full + K < pairs ? (pair_step(full + K, std::integral_constant<int, K>{}), 0) : 0), ...);
-  }(std::make_integer_sequence<int, kRing>{});
-  if (pairs % kGroupPairs != 0) flush();
-
-  // Segment sums meet in LDS, one row tile at a time:
-  // ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7)).
-  __shared__ float red[4][T][16][64];
-  // r is a compile-time index (a fold over 0 .. R - 1), so acc stays in registers.
-  auto reduce_tile = [&](auto r_const) {
-    constexpr int r = decltype(r_const)::value;
-    auto put = [&](int slot) {
-#pragma unroll
-      for (int t = 0; t < T; ++t)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) red[slot][t][v][lane] = acc[r][t][v];
-    };
-    auto take = [&](int slot) {
-#pragma unroll
-      for (int t = 0; t < T; ++t)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) acc[r][t][v] = acc[r][t][v] + red[slot][t][v][lane];
-    };
-    if constexpr (r > 0) __syncthreads();  // the previous tile's last reads of slot 2
-    if (wave & 1) put(wave / 2);
-    __syncthreads();
-    if (!(wave & 1)) take(wave / 2);  // waves 0, 2, 4, 6 hold s01, s23, s45, s67
-    if (wave == 2) put(1);
-    if (wave == 6) put(3);
-    __syncthreads();
-    if (wave == 0) take(1);  // s0123
-    if (wave == 4) take(3);  // s4567
-    if (wave == 4) put(2);
-    __syncthreads();
-    if (wave == 0) take(2);
-  };
-  [&]<int... Rs>(std::integer_sequence<int, Rs...>) {
-    (reduce_tile(std::integral_constant<int, Rs>{}), ...);
-  }(std::make_integer_sequence<int, R>{});
-  if (wave != 0) return;
-
-  // MFMA output layout: D[i][b] sits in lane b + 32 ((i / 4) % 2), register 4 (i / 8) + i % 4,
-  // so registers 4q .. 4q + 3 of a lane are four consecutive weight rows of one batch row.
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int64_t rt = rt0 + r;
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-      const int64_t b = (t0 + t) * 32 + l;
-      if (b >= a.batch) continue;
-      float* yrow = a.Y + b * a.m + rt * kRows + 4 * h;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int64_t i = rt * kRows + 8 * q + 4 * h;
-        if (i < a.m) {
-          *reinterpret_cast<float4*>(yrow + 8 * q) = make_float4(
-              acc[r][t][4 * q], acc[r][t][4 * q + 1], acc[r][t][4 * q + 2], acc[r][t][4 * q + 3]);
-        }
-      }
-    }
+    if (!has_next) break;
+    if (!chain) fill(nxt);
+    g = g_next;
+    cur = nxt;
   }
 }
 
@@ -547,33 +632,81 @@ struct PackedShape {
 
 PackedShape g_shape_override = {0, 0};
 
-// Built-in shape, from a sweep of the Llama-3-8B projections on MI355X: the largest batch tile
-// count that still gives every CU a workgroup (fewer passes over the weights); two weight tiles
-// per workgroup (each batch load serving both) from 256 batch rows on, and at 128 for the
-// middle-sized row counts (q/k/v); four batch tiles only where rows are plentiful.
-PackedShape choose_shape(int64_t row_tiles, int64_t batch) {
+// Built-in shape (R row tiles, T batch tiles per item), from sweeps of the Llama-3-8B decode
+// projections on MI355X (m = 4096, 6144, 28672 with n = 4096; m = 4096 with n = 14336) with the
+// weights streamed from HBM.  The shapes with one workgroup per CU loop over items, so what
+// matters is fewer passes over the weights (larger T), more reuse per batch load (larger R) and
+// an item count that splits evenly over the CUs:
+//   BF16, 8 batch tiles: (1, 2) for 129-255 row tiles (q/k/v: 768 items, 3 per CU), else (2, 2);
+//        4 tiles: (2, 2) from 256 row tiles, (1, 1) above 128, else (1, 2);
+//   FP8 (half the weight bytes per step, so the 4-tile items fit their registers), 8 batch
+//        tiles: (1, 1) for 129-255 row tiles, else (1, 4); 4 tiles: (1, 1) above 128 row
+//        tiles, else (1, 2).
+PackedShape choose_shape(int64_t row_tiles, int64_t batch, bool fp8) {
   if (g_shape_override.tiles > 0) return g_shape_override;
   const int64_t need = (batch + 31) / 32;
   auto groups = [&](int r, int t) { return (row_tiles + r - 1) / r * ((need + t - 1) / t); };
-  // Measured on MI355X at the Llama-3-8B decode shapes (m = 4096 .. 28672, n = 4096, 14336)
-  // with the weights streamed from HBM: at 8 batch tiles, (2, 2) unless it leaves fewer than
-  // 1024 workgroups over more than 128 row tiles; at 4 batch tiles, (2, 2) from 192 row tiles
-  // up, else (1, 2).
-  if (need >= 8) return row_tiles > 128 && groups(2, 2) < 1024 ? PackedShape{1, 1} : PackedShape{2, 2};
-  if (need >= 4) return row_tiles >= 192 ? PackedShape{2, 2} : PackedShape{1, 2};
+  const bool middle = row_tiles > 128 && row_tiles < 256;
+  if (need >= 8) {
+    if (fp8) return middle ? PackedShape{1, 1} : PackedShape{1, 4};
+    return middle ? PackedShape{1, 2} : PackedShape{2, 2};
+  }
+  if (need >= 4) {
+    if (row_tiles <= 128) return PackedShape{1, 2};
+    return fp8 || middle ? PackedShape{1, 1} : PackedShape{2, 2};
+  }
   if (need >= 2 && groups(1, 2) >= 256) return PackedShape{1, 2};
   return PackedShape{1, 1};
 }
 
-template <int R, int T>
-hipError_t launch_rt(PackedArgs a, bool fp8, hipStream_t stream) {
+// Workgroups of bgemm_packed_kernel<R, T, kFp8> to launch at most: one per CU where a CU holds
+// one, else no limit (one item per workgroup); computed once per instantiation and device.
+template <int R, int T, bool kFp8>
+hipError_t resident_groups(int64_t* out) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int64_t> cache[kMaxDevices];  // one array per instantiation
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  if (dev >= 0 && dev < kMaxDevices) {
+    const int64_t known = cache[dev].load(std::memory_order_relaxed);
+    if (known > 0) {
+      *out = known;
+      return hipSuccess;
+    }
+  }
+  int cus = 0, per_cu = 0;
+  err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (err != hipSuccess) return err;
+  err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, bgemm_packed_kernel<R, T, kFp8>,
+                                                     kThreads, 0);
+  if (err != hipSuccess) return err;
+  // With two or more workgroups per CU the others already cover one's start-up latency, and
+  // one item per workgroup measured faster there; a single resident workgroup loops.
+  const int64_t total = per_cu >= 2 ? INT64_MAX : static_cast<int64_t>(cus);
+  if (dev >= 0 && dev < kMaxDevices) cache[dev].store(total, std::memory_order_relaxed);
+  *out = total;
+  return hipSuccess;
+}
+
+template <int R, int T, bool kFp8>
+hipError_t launch_rtf(PackedArgs a, hipStream_t stream) {
   a.passes = (a.batch_tiles + T - 1) / T;
-  const int64_t groups = (a.row_tiles + R - 1) / R * a.passes;
+  const int64_t items = (a.row_tiles + R - 1) / R * a.passes;
+  if (items > 0x7FFFFFFF) return hipErrorInvalidValue;
+  int64_t resident = 0;
+  const hipError_t err = resident_groups<R, T, kFp8>(&resident);
+  if (err != hipSuccess) return err;
+  const int64_t groups = items < resident ? items : resident;
   if (groups > 0x7FFFFFFF / kThreads) return hipErrorInvalidValue;
-  const dim3 grid(static_cast<unsigned>(groups));
-  if (fp8) hipLaunchKernelGGL((bgemm_packed_kernel<R, T, true>), grid, dim3(kThreads), 0, stream, a);
-  else hipLaunchKernelGGL((bgemm_packed_kernel<R, T, false>), grid, dim3(kThreads), 0, stream, a);
+  hipLaunchKernelGGL((bgemm_packed_kernel<R, T, kFp8>), dim3(static_cast<unsigned>(groups)),
+                     dim3(kThreads), 0, stream, a);
   return hipGetLastError();
+}
+
+template <int R, int T>
+hipError_t launch_rt(const PackedArgs& a, bool fp8, hipStream_t stream) {
+  return fp8 ? launch_rtf<R, T, true>(a, stream) : launch_rtf<R, T, false>(a, stream);
 }
 
 hipError_t launch_packed(const PackedArgs& a, PackedShape shape, bool fp8, hipStream_t stream) {
@@ -655,6 +788,6 @@ extern "C" int pck_bgemm_packed(int weight_kind, const void* Wp, const void* Xp,
   if ((n / kStep) * 32 * 16 * 4 > 0x7FFFFFFFll) return hipErrorInvalidValue;
   const PackedArgs a{static_cast<const char*>(Wp), static_cast<const char*>(Xp), Y, m, n, batch,
                      row_tiles, batch_tiles, 1};
-  return launch_packed(a, choose_shape(row_tiles, batch), weight_kind == 1,
+  return launch_packed(a, choose_shape(row_tiles, batch, weight_kind == 1), weight_kind == 1,
                        static_cast<hipStream_t>(stream));
 }

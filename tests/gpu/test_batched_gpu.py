@@ -117,6 +117,47 @@ def test_every_tile_setting_gives_the_model_bits(shape: tuple[int, int], m: int,
         lib().pck_bgemm_set_shape(0, 0)
 
 
+# Far more items (R x T tiles) than the GPU holds workgroups, so each workgroup loops over
+# several: segments of a whole number of ring passes (the next item's first pairs are loaded
+# during the current one's last pass: n = 512 at two tiles, n = 1024 at three), of a partial
+# pass (n = 384: the ring is refilled at each item's start), several batch passes with the
+# row groups a multiple of 8 (m = 9728: the passes of a row group are items 8 apart), and a
+# ragged last row group and batch pass.
+LOOP_SHAPES = [((2, 2), 19200, 512, 33), ((2, 2), 19200, 384, 64), ((1, 2), 9600, 1024, 100),
+               ((1, 4), 9728, 512, 300), ((1, 1), 9612, 512, 70)]  # fmt: skip
+
+
+@pytest.mark.parametrize(("shape", "m", "n", "B"), LOOP_SHAPES, ids=str)
+def test_workgroups_looping_over_items_give_the_model_bits(shape: tuple[int, int], m: int, n: int,
+                                                           B: int) -> None:  # fmt: skip
+    """Every output equals the element kernel's (one K-step per load, no item loop, itself
+    bit-exact against the model) and a sample (three row tiles by 24 batch rows, an output
+    depending only on its own row and batch row) equals the model, BF16 and FP8."""
+    from pck.cuda._lib import lib
+
+    rng = np.random.default_rng(m + n + B)
+    W = _family(rng, (m, n), "wide")
+    X = _family(rng, (B, n), "real_x")
+    codes = rng.integers(0, 256, (m, n), dtype=np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0  # no NaN codes
+    Qv = e4m3_values()[codes].astype(np.float32)
+    tiles = (m + 31) // 32
+    sample = sorted({0, tiles // 2 + 1, tiles - 1})
+    rows = np.concatenate([np.arange(32 * t, min(32 * t + 32, m)) for t in sample])
+    bs = np.unique(np.concatenate([np.arange(8), np.arange(B // 2, B // 2 + 8), np.arange(B - 8, B)]))
+    print(f"batched items shape={shape} m={m} n={n} B={B}", flush=True)
+    try:
+        assert lib().pck_bgemm_set_shape(*shape) == 0
+        got = _run(W, X, packed=True)
+        got8 = _run_codes(codes, X, packed=True)
+    finally:
+        lib().pck_bgemm_set_shape(0, 0)
+    assert _same_bits(got, _run(W, X))
+    assert _same_bits(got8, _run_codes(codes, X, packed=False))
+    assert _same_bits(got[np.ix_(bs, rows)], emulate_batched(W[rows], X[bs]))
+    assert _same_bits(got8[np.ix_(bs, rows)], emulate_batched(Qv[rows], X[bs]))
+
+
 @pytest.mark.parametrize(("m", "n", "B"), [(64, 64, 32), (32, 8, 64)])
 def test_batched_tiny_magnitudes_match_model(m: int, n: int, B: int) -> None:
     """Products in the FP32 subnormal range; the results stay normal here (exactness of a
