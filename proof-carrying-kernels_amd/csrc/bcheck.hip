@@ -118,8 +118,10 @@ __global__ void __launch_bounds__(kThreads) partial_kernel(const Plan plan) {
   __shared__ double red[2][kWaves][kPairsWG][kColsWG + 1];  // [c.x, a.|x|][quarter][pair][col]
 
   const int64_t item = blockIdx.x;
+  // The descriptor: every comparison at once, so its loads are not a chain of dependent ones.
   int g = 0;
-  while (g + 1 < plan.count && item >= plan.start[g + 1]) ++g;
+#pragma unroll
+  for (int i = 1; i < PCK_MAX_BATCH; ++i) g += (i < plan.count && item >= plan.start[i]) ? 1 : 0;
   const PckBatchCheckDesc& d = plan.desc[g];
   const int64_t local = item - plan.start[g];
   const int64_t segments = plan.segments[g];
@@ -304,7 +306,8 @@ __global__ void __launch_bounds__(kThreads) finish_kernel(const Plan plan) {
 
   const int64_t item = blockIdx.x;
   int g = 0;
-  while (g + 1 < plan.count && item >= plan.finish[g + 1]) ++g;
+#pragma unroll
+  for (int i = 1; i < PCK_MAX_BATCH; ++i) g += (i < plan.count && item >= plan.finish[i]) ? 1 : 0;
   const PckBatchCheckDesc& d = plan.desc[g];
   const int local = static_cast<int>(item - plan.finish[g]);  // < 2^31
   const int nb = static_cast<int>(d.num_blocks);
