@@ -56,6 +56,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 8;
@@ -416,6 +417,23 @@ __global__ void __launch_bounds__(kThreads) bgemm_packed_kernel(PackedArgs a) {
   // and is the same in every wave.
   int64_t g = blockIdx.x;
   if (g >= items) return;  // uniform
+
+  // Segment sums meet in LDS without a barrier: each wave writes its sums to its own slot and
+  // counts itself in; the last of the eight to arrive adds the slots in the tree order
+  // ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7)), stores the outputs and frees the slots,
+  // while the other seven have gone on to their next item.  A wave writes an item's slot only
+  // after the previous item's slots were freed.  Slot (wave, (r T + t) 4 + q, lane) holds
+  // registers 4q .. 4q + 3 of tile (r, t): four consecutive weight rows of one batch row.
+  __shared__ f32x4 slots[kWaves][R * T * 4][64];
+  __shared__ int arrivals;  // waves that finished an item, over all items so far
+  __shared__ int freed;     // items whose slots were read
+  if (threadIdx.x == 0) {
+    arrivals = 0;
+    freed = 0;
+  }
+  __syncthreads();
+  int done = 0;  // items this wave finished (the same in every wave)
+
   Item cur = item_at(g);
   fill(cur);
   for (;;) {
@@ -514,64 +532,52 @@ __global__ void __launch_bounds__(kThreads) bgemm_packed_kernel(PackedArgs a) {
       flush();
     }
 
-    // Segment sums meet in LDS, one row tile at a time:
-    // ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7)).
-    __shared__ float red[4][T][16][64];
-    // r is a compile-time index (a fold over 0 .. R - 1), so acc stays in registers.
-    auto reduce_tile = [&](auto r_const) {
-      constexpr int r = decltype(r_const)::value;
-      auto put = [&](int slot) {
+    if (done > 0) {
+      while (__hip_atomic_load(&freed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < done)
+        __builtin_amdgcn_s_sleep(1);
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    }
 #pragma unroll
-        for (int t = 0; t < T; ++t)
+    for (int r = 0; r < R; ++r)
 #pragma unroll
-          for (int v = 0; v < 16; ++v) red[slot][t][v][lane] = acc[r][t][v];
-      };
-      auto take = [&](int slot) {
+      for (int t = 0; t < T; ++t)
 #pragma unroll
-        for (int t = 0; t < T; ++t)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) acc[r][t][v] = acc[r][t][v] + red[slot][t][v][lane];
-      };
-      __syncthreads();  // the previous tile's (or item's) last reads of the slots
-      if (wave & 1) put(wave / 2);
-      __syncthreads();
-      if (!(wave & 1)) take(wave / 2);  // waves 0, 2, 4, 6 hold s01, s23, s45, s67
-      if (wave == 2) put(1);
-      if (wave == 6) put(3);
-      __syncthreads();
-      if (wave == 0) take(1);  // s0123
-      if (wave == 4) take(3);  // s4567
-      if (wave == 4) put(2);
-      __syncthreads();
-      if (wave == 0) take(2);
-    };
-    [&]<int... Rs>(std::integer_sequence<int, Rs...>) {
-      (reduce_tile(std::integral_constant<int, Rs>{}), ...);
-    }(std::make_integer_sequence<int, R>{});
-
-    // MFMA output layout: D[i][b] sits in lane b + 32 ((i / 4) % 2), register 4 (i / 8) + i % 4,
-    // so registers 4q .. 4q + 3 of a lane are four consecutive weight rows of one batch row.
-    if (wave == 0) {
+        for (int q = 0; q < 4; ++q)
+          slots[wave][(r * T + t) * 4 + q][lane] =
+              f32x4{acc[r][t][4 * q], acc[r][t][4 * q + 1], acc[r][t][4 * q + 2], acc[r][t][4 * q + 3]};
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    // One count per wave: lane 0 adds, every lane takes its result.
+    int arrived = 0;
+    if (lane == 0)
+      arrived = __hip_atomic_fetch_add(&arrivals, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    arrived = __builtin_amdgcn_readfirstlane(arrived);
+    if (arrived == kWaves * done + kWaves - 1) {  // uniform: the last wave of this item
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+      // MFMA output layout: D[i][b] sits in lane b + 32 ((i / 4) % 2), register 4 (i / 8) + i % 4.
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int64_t rt = cur.rt0 + r;
 #pragma unroll
         for (int t = 0; t < T; ++t) {
           const int64_t b = (cur.t0 + t) * 32 + l;
-          if (b >= a.batch) continue;
           float* yrow = a.Y + b * a.m + rt * kRows + 4 * h;
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
+            const int k = (r * T + t) * 4 + q;
+            const f32x4 y = ((slots[0][k][lane] + slots[1][k][lane]) +
+                             (slots[2][k][lane] + slots[3][k][lane])) +
+                            ((slots[4][k][lane] + slots[5][k][lane]) +
+                             (slots[6][k][lane] + slots[7][k][lane]));
             const int64_t i = rt * kRows + 8 * q + 4 * h;
-            if (i < a.m) {
-              *reinterpret_cast<float4*>(yrow + 8 * q) =
-                  make_float4(acc[r][t][4 * q], acc[r][t][4 * q + 1], acc[r][t][4 * q + 2],
-                              acc[r][t][4 * q + 3]);
-            }
+            if (b < a.batch && i < a.m)
+              *reinterpret_cast<float4*>(yrow + 8 * q) = make_float4(y[0], y[1], y[2], y[3]);
           }
         }
       }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+      __hip_atomic_store(&freed, done + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
+    ++done;
     if (!has_next) break;
     if (!chain) fill(nxt);
     g = g_next;
