@@ -640,26 +640,21 @@ PackedShape g_shape_override = {0, 0};
 
 // Built-in shape (R row tiles, T batch tiles per item), from sweeps of the Llama-3-8B decode
 // projections on MI355X (m = 4096, 6144, 28672 with n = 4096; m = 4096 with n = 14336) with the
-// weights streamed from HBM.  The shapes with one workgroup per CU loop over items, so what
-// matters is fewer passes over the weights (larger T), more reuse per batch load (larger R) and
-// an item count that splits evenly over the CUs:
-//   BF16, 8 batch tiles: (1, 2) for 129-255 row tiles (q/k/v: 768 items, 3 per CU), else (2, 2);
-//        4 tiles: (2, 2) from 256 row tiles, (1, 1) above 128, else (1, 2);
-//   FP8 (half the weight bytes per step, so the 4-tile items fit their registers), 8 batch
-//        tiles: (1, 1) for 129-255 row tiles, else (1, 4); 4 tiles: (1, 1) above 128 row
-//        tiles, else (1, 2).
+// weights streamed from HBM (about 600 MB of distinct weight copies per launch).  The shapes
+// with one workgroup per CU loop over items, so what matters is fewer passes over the weights
+// (larger T), more reuse per batch load (larger R) and an item count that splits evenly:
+//   (1, 2) for at most 128 row tiles at 4 batch tiles (o, down at B = 128), and for 129-255
+//          row tiles at 8 (q/k/v at B = 256: 768 items, 3 per CU);
+//   else (2, 2) for BF16 and (1, 4) for FP8, whose half-size weight steps leave the registers
+//          for four batch tiles.
 PackedShape choose_shape(int64_t row_tiles, int64_t batch, bool fp8) {
   if (g_shape_override.tiles > 0) return g_shape_override;
   const int64_t need = (batch + 31) / 32;
   auto groups = [&](int r, int t) { return (row_tiles + r - 1) / r * ((need + t - 1) / t); };
-  const bool middle = row_tiles > 128 && row_tiles < 256;
-  if (need >= 8) {
-    if (fp8) return middle ? PackedShape{1, 1} : PackedShape{1, 4};
-    return middle ? PackedShape{1, 2} : PackedShape{2, 2};
-  }
   if (need >= 4) {
-    if (row_tiles <= 128) return PackedShape{1, 2};
-    return fp8 || middle ? PackedShape{1, 1} : PackedShape{2, 2};
+    const bool middle = row_tiles > 128 && row_tiles < 256;
+    if (need >= 8 ? middle : row_tiles <= 128) return PackedShape{1, 2};
+    return fp8 ? PackedShape{1, 4} : PackedShape{2, 2};
   }
   if (need >= 2 && groups(1, 2) >= 256) return PackedShape{1, 2};
   return PackedShape{1, 1};
