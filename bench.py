@@ -352,8 +352,9 @@ def b1_modes(layers, depth: int, rounds: int, modes=MODES) -> tuple[dict, dict]:
 def dominant_launch_ms(layers, reps: int, inpass: bool = False) -> tuple[float, int]:  # type: ignore[no-untyped-def]
     """Mean duration of the dominant kernel's launches (the q/k/v, o and gate/up groups; with
     ``inpass`` the in-pass kernel, row sums included) replayed back to back from one graph over
-    every layer copy, timed with HIP events on the stream the launches run on, and their mean
-    algorithmic bytes."""
+    every layer copy, timed with HIP events on the stream the launches run on (each replay on
+    its own; the median replay, so that one disturbed replay does not move the figure), and
+    their mean algorithmic bytes."""
     import torch
 
     from pck.cuda import gemv_group, gemv_group_rowsums
@@ -380,14 +381,15 @@ def dominant_launch_ms(layers, reps: int, inpass: bool = False) -> tuple[float, 
     for _ in range(3):
         g.replay()
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(reps):
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(reps)]  # fmt: skip
+    for start, end in events:
+        start.record()
         g.replay()
-    end.record()
+        end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / (reps * len(dom) * len(layers)), nbytes // len(dom)
+    per_replay = statistics.median(start.elapsed_time(end) for start, end in events)
+    return per_replay / (len(dom) * len(layers)), nbytes // len(dom)
 
 
 def timed(layers, steps: int, warmup: int, with_check: bool, per_kernel: bool):  # type: ignore[no-untyped-def]
@@ -1095,7 +1097,7 @@ def b1_section(fp8: bool, copies: int, depth: int, rounds: int, quick: bool, ste
         "gemv_only_pct_of_size_matched_read": round(100 * matched_ms / base, 2),
     }
     if not fp8:
-        reps = max(10, steps // 10)
+        reps = max(21, steps // 10)
         out["dominant"] = dominant_launch_ms(layers, reps)
         out["dominant_inpass"] = dominant_launch_ms(layers, reps, inpass=True)
         if not quick:
