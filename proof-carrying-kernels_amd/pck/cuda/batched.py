@@ -97,10 +97,13 @@ def pack_batched_weights(W: torch.Tensor) -> BatchedWeights:
     return BatchedWeights(m, n, W.dtype, _pack(W, _kind(W.dtype)), None)
 
 
-def gemm_batched(W: torch.Tensor | BatchedWeights, X: torch.Tensor) -> torch.Tensor:
+def gemm_batched(
+    W: torch.Tensor | BatchedWeights, X: torch.Tensor, out: torch.Tensor | None = None
+) -> torch.Tensor:
     """Y (B, m) FP32 = X (B, n) BF16 times W^T for W (m, n) BF16 or float8_e4m3fn (raw codes;
     row scales are the caller's, as for `gemv_fp8`), or W packed by `pack_batched_weights`.
-    Enqueued on the current stream."""
+    Enqueued on the current stream; written into ``out`` (a contiguous (B, m) float32 tensor on
+    W's device) when given, so that a check of Y can be planned before the product runs."""
     packed = isinstance(W, BatchedWeights)
     if packed:
         m, n, dtype, device = W.m, W.n, W.dtype, W.device
@@ -122,7 +125,13 @@ def gemm_batched(W: torch.Tensor | BatchedWeights, X: torch.Tensor) -> torch.Ten
     if (not packed and not W.is_contiguous()) or not X.is_contiguous():
         raise RuntimeError("W and X must be contiguous")
     B = X.size(0)
-    Y = torch.empty((B, m), dtype=torch.float32, device=device)
+    if out is None:
+        Y = torch.empty((B, m), dtype=torch.float32, device=device)
+    else:
+        if not (out.is_cuda and out.device == device and out.dtype == torch.float32
+                and out.shape == (B, m) and out.is_contiguous()):  # fmt: skip
+            raise RuntimeError(f"out must be a contiguous ({B}, {m}) float32 tensor on {device}")
+        Y = out
     if m == 0 or B == 0:
         return Y
     if n == 0:

@@ -231,6 +231,25 @@ def test_batched_height_formula() -> None:
         assert batched_height(n) == oracle_height(n)
 
 
+def test_batched_writes_into_a_given_output() -> None:
+    """gemm_batched(..., out=Y) writes the product's bits into Y and returns it, on both
+    routes; a wrong shape, dtype or layout is refused."""
+    rng = np.random.default_rng(5)
+    W = _family(rng, (96, 512), "real_w")
+    X = _family(rng, (40, 512), "real_x")
+    Wt, Xt = _bf16_tensor(W), _bf16_tensor(X)
+    for w in (Wt, pack_batched_weights(Wt)):
+        Y = torch.full((40, 96), float("nan"), dtype=torch.float32, device=DEV)
+        got = gemm_batched(w, Xt, out=Y)
+        torch.cuda.synchronize()
+        assert got is Y
+        assert _same_bits(Y.cpu().numpy(), emulate_batched(W, X))
+        for bad in (torch.empty(40, 95, device=DEV), torch.empty(40, 96, dtype=torch.float64, device=DEV),
+                    torch.empty(96, 40, device=DEV).t()):  # fmt: skip
+            with pytest.raises(RuntimeError, match="out must be"):
+                gemm_batched(w, Xt, out=bad)
+
+
 def test_batched_validation_messages() -> None:
     W = torch.zeros(4, 8, dtype=torch.bfloat16, device=DEV)
     X = torch.zeros(2, 8, dtype=torch.bfloat16, device=DEV)
