@@ -290,18 +290,21 @@ struct PackedArgs {
 
 // R row tiles (32 weight rows each) and T batch tiles per item: every wave multiplies its K
 // segment of R weight tiles by the same T batch tiles, so each batch load serves R tiles.
+// Step pairs in flight per lane: four, or two for four-tile items, whose accumulators leave
+// the registers for only two (more would spill at two waves per SIMD).
 template <int R, int T>
 constexpr int ring_pairs() {
   return R + T >= 4 ? 2 : 4;
 }
 
-// An item is one (row group, batch pass): R row tiles by T batch tiles.  The grid holds as
-// many workgroups as the GPU keeps resident, and workgroup w takes items w, w + G, w + 2 G, ...
-// (G workgroups).  During an item's last ring pass the refills already fetch the next item's
-// first step pairs, so only a workgroup's first item waits a full memory latency before its
-// first step.  Item g -> (row group, pass): with the groups a multiple of 8, the passes of a
-// row group are items 8 apart, which run at about the same time on one XCD (workgroup w runs
-// on XCD w % 8 when G is a multiple of 8), so their repeated weight reads hit that XCD's L2.
+// An item is one (row group, batch pass): R row tiles by T batch tiles.  Where a CU holds one
+// workgroup of this kernel, the grid is one workgroup per CU and workgroup w takes items w,
+// w + G, w + 2 G, ... (G workgroups); elsewhere each workgroup takes one item.  During an
+// item's last ring pass the refills already fetch the next item's first step pairs, so only a
+// workgroup's first item waits a full memory latency before its first step.  Item g ->
+// (row group, pass): with the groups a multiple of 8, the passes of a row group are items 8
+// apart, which run at about the same time on one XCD (workgroup w runs on XCD w % 8 when G is
+// a multiple of 8), so their repeated weight reads hit that XCD's L2.
 template <int R, int T, bool kFp8>
 __global__ void __launch_bounds__(kThreads) bgemm_packed_kernel(PackedArgs a) {
   constexpr uint32_t kQ = kFp8 ? 8 : 16;  // weight bytes per lane and step pair
