@@ -50,6 +50,7 @@
 
 #include <atomic>
 
+#include <climits>
 #include <cstdint>
 #include <utility>
 
@@ -79,7 +80,49 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
+// What a partial workgroup needs of its descriptor, in 64 bytes that load together (every
+// count fits in 32 bits: the plan bounds pairs x n x 4 and batch x n x 2 below 2^31).
+struct PartialDesc {
+  const float* c;
+  const void* a;
+  const void* X;
+  int64_t slot;        // the descriptor's first workspace entry
+  int32_t start;       // its first partial workgroup
+  int32_t segments;    // K segments
+  int32_t pair_tiles;  // tiles of kPairsWG pairs
+  int32_t pairs;       // checks x num_blocks
+  int32_t num_blocks;
+  int32_t n;
+  int32_t batch;
+  int32_t unused;
+};
+static_assert(sizeof(PartialDesc) == 64, "one 64-byte record per descriptor");
+
+// What a finish workgroup needs of its descriptor for its loads, in 64 bytes.
+struct FinishDesc {
+  const float* Y;
+  const int8_t* r;
+  int64_t slot;     // the descriptor's first workspace entry
+  int64_t outs;     // checks x num_blocks x batch: the stride of one segment's partials
+  int32_t start;    // its first finish workgroup
+  int32_t num_blocks;
+  int32_t block;
+  int32_t checks;
+  int32_t batch;
+  int32_t segments;
+  int32_t n;
+  int32_t unused;
+};
+static_assert(sizeof(FinishDesc) == 64, "one 64-byte record per descriptor");
+
 struct Plan {
+  PartialDesc part[PCK_MAX_BATCH];
+  FinishDesc fin[PCK_MAX_BATCH];
+  // The descriptor searches' bounds in 32 bits (one load each; the launch checks both grids
+  // are below 2^31): the first partial and finish workgroup of descriptors 1 .. count - 1,
+  // INT32_MAX past the count.
+  int32_t part_first[PCK_MAX_BATCH];
+  int32_t fin_first[PCK_MAX_BATCH];
   PckBatchCheckDesc desc[PCK_MAX_BATCH];
   int64_t start[PCK_MAX_BATCH + 1];   // partial workgroups, prefix sums
   int64_t finish[PCK_MAX_BATCH + 1];  // finish workgroups (blocks x column groups), prefix
@@ -117,26 +160,35 @@ __device__ __forceinline__ bf16x8 abs_floor8(u32x4 v) {
 __global__ void __launch_bounds__(kThreads) partial_kernel(const Plan plan) {
   __shared__ double red[2][kWaves][kPairsWG][kColsWG + 1];  // [c.x, a.|x|][quarter][pair][col]
 
-  const int64_t item = blockIdx.x;
-  // The descriptor: every comparison at once, so its loads are not a chain of dependent ones.
+  const int item = static_cast<int>(blockIdx.x);  // the launch checks the grid is < 2^31
+  // The descriptor: every comparison at once, so its loads are not a chain of dependent ones;
+  // then its whole record in one round trip.
+  // Every value below is needed before the first operand load.  Empty asm statements that
+  // read them make the compiler request them together: the plan's own fields with the search
+  // bounds, then the descriptor's record, two round trips instead of one per use.
+  double* const part_cx = plan.part_cx;
+  double* const part_s = plan.part_s;
+  const int seg_len = static_cast<int>(plan.seg_len);  // at most n rounded up to the quantum
   int g = 0;
 #pragma unroll
-  for (int i = 1; i < PCK_MAX_BATCH; ++i) g += (i < plan.count && item >= plan.start[i]) ? 1 : 0;
-  const PckBatchCheckDesc& d = plan.desc[g];
-  const int64_t local = item - plan.start[g];
-  const int64_t segments = plan.segments[g];
-  const int64_t seg = local % segments;
-  const int64_t tile = local / segments;
-  const int64_t pair0 = (tile % plan.pair_tiles[g]) * kPairsWG;
-  const int64_t col0 = (tile / plan.pair_tiles[g]) * kColsWG;
-  const int64_t pairs = d.checks * d.num_blocks;
-  const int64_t n = d.n;
+  for (int i = 1; i < PCK_MAX_BATCH; ++i) g += item >= plan.part_first[i] ? 1 : 0;
+  __asm__ volatile("" ::"s"(part_cx), "s"(part_s), "s"(seg_len));
+  const PartialDesc p = plan.part[g];
+  __asm__ volatile("" ::"s"(p.c), "s"(p.a), "s"(p.X), "s"(p.slot), "s"(p.start), "s"(p.segments),
+                   "s"(p.pair_tiles), "s"(p.pairs), "s"(p.num_blocks), "s"(p.n), "s"(p.batch));
+  const int local = item - p.start;
+  const int seg = local % p.segments;
+  const int tile = local / p.segments;
+  const int pair0 = (tile % p.pair_tiles) * kPairsWG;
+  const int col0 = (tile / p.pair_tiles) * kColsWG;
+  const int pairs = p.pairs;
+  const int n = p.n;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / 64);
-  const int64_t quarter = plan.seg_len / kWaves;
-  const int64_t j_seg_hi = (seg + 1) * plan.seg_len < n ? (seg + 1) * plan.seg_len : n;
-  const int64_t j_lo = seg * plan.seg_len + wave * quarter;
-  const int64_t j_hi = j_lo + quarter < j_seg_hi ? j_lo + quarter : j_seg_hi;
-  const int steps = j_hi > j_lo ? static_cast<int>((j_hi - j_lo + kStep - 1) / kStep) : 0;
+  const int quarter = seg_len / kWaves;
+  const int j_seg_hi = (seg + 1) * seg_len < n ? (seg + 1) * seg_len : n;
+  const int j_lo = seg * seg_len + wave * quarter;
+  const int j_hi = j_lo + quarter < j_seg_hi ? j_lo + quarter : j_seg_hi;
+  const int steps = j_hi > j_lo ? (j_hi - j_lo + kStep - 1) / kStep : 0;
 
   // Lane l = 16 q + i supplies row i of the A tiles (bank rows) and column i of the B tiles
   // (batch rows) at the step's columns 8 q .. 8 q + 7: FP64 step e takes column 8 q + e as its
@@ -146,34 +198,40 @@ __global__ void __launch_bounds__(kThreads) partial_kernel(const Plan plan) {
   // bound is a multiple of 8: a lane's eight columns are all in or all out).
   const int lane = static_cast<int>(threadIdx.x) % 64;
   const int li = lane % 16, lq = lane / 16;
-  const __amdgpu_buffer_rsrc_t rc = check::make_rsrc(d.c, static_cast<uint32_t>(pairs * n * 4));
+  const __amdgpu_buffer_rsrc_t rc = check::make_rsrc(p.c, static_cast<uint32_t>(pairs * n * 4));
   const __amdgpu_buffer_rsrc_t ra =
-      check::make_rsrc(d.a, static_cast<uint32_t>(d.num_blocks * n * 2));
-  const __amdgpu_buffer_rsrc_t rx = check::make_rsrc(d.X, static_cast<uint32_t>(d.batch * n * 2));
-  const int64_t j_lane = j_lo + 8 * lq;
+      check::make_rsrc(p.a, static_cast<uint32_t>(p.num_blocks * n * 2));
+  const __amdgpu_buffer_rsrc_t rx = check::make_rsrc(p.X, static_cast<uint32_t>(p.batch * n * 2));
+  const int j_lane = j_lo + 8 * lq;
   uint32_t c_voff[2], a_voff[2], x_voff[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const int64_t pair = pair0 + kTile * t + li;
-    const int64_t col = col0 + kTile * t + li;
-    c_voff[t] = pair < pairs ? static_cast<uint32_t>((pair * n + j_lane) * 4) : check::kOutOfRange;
-    a_voff[t] = pair < pairs ? static_cast<uint32_t>(((pair % d.num_blocks) * n + j_lane) * 2)
+    const int pair = pair0 + kTile * t + li;
+    const int col = col0 + kTile * t + li;
+    // unsigned: a lane past n (a wave with no steps) stays below 2^32
+    const uint32_t jl = static_cast<uint32_t>(j_lane), un = static_cast<uint32_t>(n);
+    c_voff[t] = pair < pairs ? (static_cast<uint32_t>(pair) * un + jl) * 4u : check::kOutOfRange;
+    a_voff[t] = pair < pairs ? (static_cast<uint32_t>(pair % p.num_blocks) * un + jl) * 2u
                              : check::kOutOfRange;
-    x_voff[t] = col < d.batch ? static_cast<uint32_t>((col * n + j_lane) * 2) : check::kOutOfRange;
+    x_voff[t] = col < p.batch ? (static_cast<uint32_t>(col) * un + jl) * 2u : check::kOutOfRange;
   }
 
   auto fetch = [&](int step) {
     const int st = step < steps ? step : (steps > 0 ? steps - 1 : 0);  // past the end: unused
     const uint32_t at = static_cast<uint32_t>(st) * kStep;
-    // the select is on the offset, so nothing waits for the load here
-    const bool in = j_lane + static_cast<int64_t>(st) * kStep < j_hi;
+    // A lane past the quarter's end sets the offset's top bit, which puts every load past its
+    // buffer (below 2^31 bytes), so it reads zero.  The bit is opaque to the compiler (an empty
+    // asm), so the loads stay unconditional: a select between two offsets was compiled into
+    // branches, each load behind a wait for every load in flight.
+    uint32_t out = j_lane + st * kStep < j_hi ? 0u : check::kOutOfRange;
+    __asm__("" : "+v"(out));
     Staged v;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      v.c[t][0] = load_b128(rc, in ? c_voff[t] + at * 4 : check::kOutOfRange);
-      v.c[t][1] = load_b128(rc, in ? c_voff[t] + at * 4 + 16 : check::kOutOfRange);
-      v.a[t] = load_b128(ra, in ? a_voff[t] + at * 2 : check::kOutOfRange);
-      v.x[t] = load_b128(rx, in ? x_voff[t] + at * 2 : check::kOutOfRange);
+      v.c[t][0] = load_b128(rc, (c_voff[t] + at * 4) | out);
+      v.c[t][1] = load_b128(rc, (c_voff[t] + at * 4 + 16) | out);
+      v.a[t] = load_b128(ra, (a_voff[t] + at * 2) | out);
+      v.x[t] = load_b128(rx, (x_voff[t] + at * 2) | out);
     }
     return v;
   };
@@ -223,14 +281,17 @@ __global__ void __launch_bounds__(kThreads) partial_kernel(const Plan plan) {
 
   // Step q is consumed from ring slot q % kRing, which is then refilled with step q + kRing.
   // Whole ring passes have no exit inside, so the loads in flight are the same on every entry
-  // to the loop head.
+  // to the loop head.  A scheduling barrier after each refill keeps its loads ahead of the next
+  // slot's products (the scheduler otherwise sinks them to the end of the pass, leaving no
+  // load in flight while the last slot is consumed).
   Staged ring[kRing];
 #pragma unroll
   for (int k = 0; k < kRing; ++k) ring[k] = fetch(k);
   const int full = steps / kRing * kRing;
   for (int base = 0; base < full; base += kRing) {
     [&]<int... K>(std::integer_sequence<int, K...>) {
-      ((consume(ring[K]), ring[K] = fetch(base + K + kRing)), ...);
+      ((consume(ring[K]), ring[K] = fetch(base + K + kRing), __builtin_amdgcn_sched_barrier(0)),
+       ...);
     }(std::make_integer_sequence<int, kRing>{});
   }
   [&]<int... K>(std::integer_sequence<int, K...>) {
@@ -249,19 +310,20 @@ __global__ void __launch_bounds__(kThreads) partial_kernel(const Plan plan) {
         red[1][wave][kTile * t + 4 * lq + r][kTile * u + li] = s[t][u][r];
       }
   __syncthreads();
-  const int64_t outs = pairs * d.batch;
-  double* dst_cx = plan.part_cx + plan.slots[g] + seg * outs;
-  double* dst_s = plan.part_s + plan.slots[g] + seg * outs;
+  const int64_t outs = static_cast<int64_t>(pairs) * p.batch;
+  double* dst_cx = part_cx + p.slot + seg * outs;
+  double* dst_s = part_s + p.slot + seg * outs;
   const int t = static_cast<int>(threadIdx.x);
 #pragma unroll
   for (int i = 0; i < kPairsWG * kColsWG / kThreads; ++i) {
     const int o = t + kThreads * i;
     const int pr = o / kColsWG, cl = o % kColsWG;
-    const int64_t pair = pair0 + pr, col = col0 + cl;
-    if (pair < pairs && col < d.batch) {
-      dst_cx[pair * d.batch + col] =
+    const int pair = pair0 + pr, col = col0 + cl;
+    if (pair < pairs && col < p.batch) {
+      const int64_t at = static_cast<int64_t>(pair) * p.batch + col;
+      dst_cx[at] =
           (red[0][0][pr][cl] + red[0][1][pr][cl]) + (red[0][2][pr][cl] + red[0][3][pr][cl]);
-      dst_s[pair * d.batch + col] =
+      dst_s[at] =
           (red[1][0][pr][cl] + red[1][1][pr][cl]) + (red[1][2][pr][cl] + red[1][3][pr][cl]);
     }
   }
@@ -304,86 +366,127 @@ __global__ void __launch_bounds__(kThreads) finish_kernel(const Plan plan) {
   __shared__ double red_ry[kFinishCols], red_yabs[kFinishCols];
   __shared__ double red_cx[kSubsets][kFinishCols], red_s[kSubsets][kFinishCols];
 
-  const int64_t item = blockIdx.x;
+  const int item = static_cast<int>(blockIdx.x);  // the launch checks the grid is < 2^31
+  // The plan's fields with the search bounds, then the record: two round trips (see the
+  // partial kernel).
+  const double* const part_cx = plan.part_cx;
+  const double* const part_s = plan.part_s;
   int g = 0;
 #pragma unroll
-  for (int i = 1; i < PCK_MAX_BATCH; ++i) g += (i < plan.count && item >= plan.finish[i]) ? 1 : 0;
-  const PckBatchCheckDesc& d = plan.desc[g];
-  const int local = static_cast<int>(item - plan.finish[g]);  // < 2^31
-  const int nb = static_cast<int>(d.num_blocks);
+  for (int i = 1; i < PCK_MAX_BATCH; ++i) g += item >= plan.fin_first[i] ? 1 : 0;
+  __asm__ volatile("" ::"s"(part_cx), "s"(part_s));
+  const FinishDesc f = plan.fin[g];
+  __asm__ volatile("" ::"s"(f.Y), "s"(f.r), "s"(f.slot), "s"(f.outs), "s"(f.start),
+                   "s"(f.num_blocks), "s"(f.block), "s"(f.checks), "s"(f.batch), "s"(f.segments));
+  const int local = item - f.start;
+  const int nb = f.num_blocks;
   const int beta = local % nb;
-  const int64_t col0 = static_cast<int64_t>(local / nb) * kFinishCols;
+  const int col0 = (local / nb) * kFinishCols;
   const int t = static_cast<int>(threadIdx.x);
   const int row = t / kFinishLanes, q = t % kFinishLanes;
-  const int64_t m = d.num_blocks * d.block;
-  const int groups = static_cast<int>(d.block / 4);  // block % 4 == 0
-  const int segments = static_cast<int>(plan.segments[g]);
-  const int64_t outs = d.checks * d.num_blocks * d.batch;
-  // Every load below is unconditional, at a valid address (a column past the batch reads
-  // column 0, a group or segment past the end reads the last one), and data that is not needed
-  // is dropped where it is used: a conditional load would be followed by a wait for it before
-  // the next one could be issued.  The sums of columns past the batch are computed and never
-  // read.
-  const float4* ycol[kRowCols];
+  const int64_t m = static_cast<int64_t>(nb) * f.block;
+  const int groups = f.block / 4;  // block % 4 == 0
+  const int segments = f.segments;
+  const int cols = f.batch - col0 < kFinishCols ? f.batch - col0 : kFinishCols;  // >= 1
+  // Every load below is an unconditional raw buffer load at a valid address: a uniform base
+  // and a 32-bit lane offset (the plan bounds every range below 2^31 bytes).  A column past
+  // the batch reads the last column, a group or segment past the end reads the last one, and
+  // data that is not needed is dropped where it is used, by a select on the value: a
+  // conditional load would be followed by a wait for it before the next one could be issued.
+  // The sums of columns past the batch are computed and never read.
+  //   Outputs: from the workgroup's first column of the block; column j of row r at
+  //   (min(r + 16 j, cols - 1) m) x 4 bytes.
+  const __amdgpu_buffer_rsrc_t y_rsrc = check::make_rsrc(
+      f.Y + static_cast<int64_t>(col0) * m + static_cast<int64_t>(beta) * f.block,
+      static_cast<uint32_t>(((cols - 1) * m + f.block) * 4));
+  uint32_t y_off[kRowCols];
 #pragma unroll
   for (int j = 0; j < kRowCols; ++j) {
-    const int64_t col = col0 + row + kFinishLanes * j;
-    ycol[j] = reinterpret_cast<const float4*>(d.Y + (col < d.batch ? col : 0) * m + beta * d.block);
+    const int c = row + kFinishLanes * j < cols ? row + kFinishLanes * j : cols - 1;
+    y_off[j] = static_cast<uint32_t>(c * m * 4);
   }
 
   // sum |y| to nearest, at most block / 16 + 4 additions deep, then raised by 1 + (b + 4) 2^-52
   // (the factor is exact in FP64)
-  const double yabs_slack = 1.0 + static_cast<double>(d.block + 4) * 0x1p-52;
+  const double yabs_slack = 1.0 + static_cast<double>(f.block + 4) * 0x1p-52;
   double yabs[kRowCols] = {};
-  const int pc = t % kFinishCols, sub = t / kFinishCols;  // partials: column, segment subset
-  const bool pin = col0 + pc < d.batch;
+  const int pc = t % kFinishCols;  // partials: this lane's column
+  const int sub = __builtin_amdgcn_readfirstlane(t / kFinishCols);  // and its segment subset
+  const uint32_t p_off = static_cast<uint32_t>((pc < cols ? pc : cols - 1) * 8);
+  const uint32_t seg_bytes = static_cast<uint32_t>(f.outs * 8);  // one segment's partials
   constexpr int kAhead = 8;
-  for (int64_t k = 0; k < d.checks; ++k) {
-    const int64_t pair = k * d.num_blocks + beta;
-    const uint32_t* sign = reinterpret_cast<const uint32_t*>(d.r + pair * d.block);
-    // The first pass of this lane's partials (column t % 64, segments t / 64, t / 64 + 4, ...)
-    // is requested before the outputs, so both reads are in flight together.
-    const int64_t pat = pair * d.batch + (pin ? col0 + pc : 0);
-    const double* pcx = plan.part_cx + plan.slots[g] + pat;
-    const double* ps = plan.part_s + plan.slots[g] + pat;
+  int k = 0;
+  do {  // checks >= 1 (the plan rejects fewer)
+    const int64_t pair = static_cast<int64_t>(k) * nb + beta;
+    const __amdgpu_buffer_rsrc_t r_rsrc =
+        check::make_rsrc(f.r + pair * f.block, static_cast<uint32_t>(f.block));
+    // One pass of outputs: float4 groups i0, i0 + 16 of the block in each of the row's columns,
+    // and their signs.
+    f32x4 v[kRowCols][kPass];
+    uint32_t sg[kPass];
+    auto load_pass = [&](int i0) {
+#pragma unroll
+      for (int e = 0; e < kPass; ++e) {
+        const int i = i0 + kFinishLanes * e < groups ? i0 + kFinishLanes * e : groups - 1;
+        sg[e] = __builtin_amdgcn_raw_buffer_load_b32(r_rsrc, i * 4, 0, 0);
+#pragma unroll
+        for (int j = 0; j < kRowCols; ++j)
+          v[j][e] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(y_rsrc, y_off[j] + i * 16, 0, 0));
+      }
+    };
+    double ry[kRowCols] = {};
+    const bool first = k == 0;  // sum |y| once, over the first check's pass
+    auto use_pass = [&](int i0) {
+#pragma unroll
+      for (int e = 0; e < kPass; ++e) {
+        const bool in = i0 + kFinishLanes * e < groups;  // groups past the end add nothing
+#pragma unroll
+        for (int j = 0; j < kRowCols; ++j) {
+#pragma unroll
+          for (int h = 0; h < 4; ++h) {
+            // A skipped term adds +0.0, which leaves the sum unchanged: it starts at +0 and
+            // never becomes -0 under round-to-nearest.
+            const double yd = static_cast<double>(v[j][e][h]);
+            const bool plus = static_cast<int8_t>((sg[e] >> (8 * h)) & 0xFFu) > 0;
+            ry[j] = ry[j] + (in ? (plus ? yd : -yd) : 0.0);
+            yabs[j] = yabs[j] + (in && first ? __builtin_fabs(yd) : 0.0);
+          }
+        }
+      }
+    };
+    // The first pass of outputs is requested first, then this lane's first pass of partials
+    // (column t % 64, segments t / 64, t / 64 + 4, ...): loads complete in the order they are
+    // issued, so the outputs, used first, wait for nothing behind them.
+    load_pass(q);
+    const __amdgpu_buffer_rsrc_t cx_rsrc = check::make_rsrc(
+        part_cx + f.slot + pair * f.batch + col0,
+        static_cast<uint32_t>((segments - 1) * f.outs * 8 + cols * 8));
+    const __amdgpu_buffer_rsrc_t s_rsrc = check::make_rsrc(
+        part_s + f.slot + pair * f.batch + col0,
+        static_cast<uint32_t>((segments - 1) * f.outs * 8 + cols * 8));
+    auto load_partial = [&](const __amdgpu_buffer_rsrc_t& rs, int sgi) {
+      return __builtin_bit_cast(
+          double, __builtin_amdgcn_raw_buffer_load_b64(rs, static_cast<int>(p_off),
+                                                       static_cast<int>(sgi * seg_bytes), 0));
+    };
     double vc[kAhead], vs[kAhead];
 #pragma unroll
     for (int e = 0; e < kAhead; ++e) {
       const int sgi = sub + kSubsets * e < segments ? sub + kSubsets * e : segments - 1;
-      vc[e] = pcx[sgi * outs];
-      vs[e] = ps[sgi * outs];
+      vc[e] = load_partial(cx_rsrc, sgi);
+      vs[e] = load_partial(s_rsrc, sgi);
     }
-    double ry[kRowCols] = {};
-    for (int i0 = q; i0 < groups; i0 += kPass * kFinishLanes) {
-      float4 v[kRowCols][kPass];
-      uint32_t sg[kPass];
-#pragma unroll
-      for (int e = 0; e < kPass; ++e) {
-        const int i = i0 + kFinishLanes * e < groups ? i0 + kFinishLanes * e : groups - 1;
-        sg[e] = sign[i];
-#pragma unroll
-        for (int j = 0; j < kRowCols; ++j) v[j][e] = ycol[j][i];
-      }
-#pragma unroll
-      for (int e = 0; e < kPass; ++e) {
-        if (i0 + kFinishLanes * e >= groups) break;
-#pragma unroll
-        for (int j = 0; j < kRowCols; ++j) {
-          const float f[4] = {v[j][e].x, v[j][e].y, v[j][e].z, v[j][e].w};
-#pragma unroll
-          for (int h = 0; h < 4; ++h) {
-            const double yd = static_cast<double>(f[h]);
-            const bool plus = static_cast<int8_t>((sg[e] >> (8 * h)) & 0xFFu) > 0;
-            ry[j] = ry[j] + (plus ? yd : -yd);
-            if (k == 0) yabs[j] = yabs[j] + __builtin_fabs(yd);
-          }
-        }
-      }
+    __builtin_amdgcn_sched_barrier(0);
+    use_pass(q);
+    for (int i0 = q + kPass * kFinishLanes; i0 < groups; i0 += kPass * kFinishLanes) {
+      load_pass(i0);
+      use_pass(i0);
     }
 #pragma unroll
     for (int j = 0; j < kRowCols; ++j) {
       ry[j] = row_sum(ry[j]);
-      if (k == 0) yabs[j] = mul_up_nonneg(row_sum(yabs[j]), yabs_slack);
+      if (first) yabs[j] = mul_up_nonneg(row_sum(yabs[j]), yabs_slack);
       if (q == 0) {
         red_ry[row + kFinishLanes * j] = ry[j];
         red_yabs[row + kFinishLanes * j] = yabs[j];
@@ -396,41 +499,42 @@ __global__ void __launch_bounds__(kThreads) finish_kernel(const Plan plan) {
       for (int s0 = sub;;) {
 #pragma unroll
         for (int e = 0; e < kAhead; ++e) {
-          if (s0 + kSubsets * e >= segments) break;
-          cx = cx + vc[e];
-          s = s + vs[e];
+          const bool in = s0 + kSubsets * e < segments;  // past the end: + 0.0, as above
+          cx = cx + (in ? vc[e] : 0.0);
+          s = s + (in ? vs[e] : 0.0);
         }
         s0 += kAhead * kSubsets;
         if (s0 >= segments) break;
 #pragma unroll
         for (int e = 0; e < kAhead; ++e) {
           const int sgi = s0 + kSubsets * e < segments ? s0 + kSubsets * e : segments - 1;
-          vc[e] = pcx[sgi * outs];
-          vs[e] = ps[sgi * outs];
+          vc[e] = load_partial(cx_rsrc, sgi);
+          vs[e] = load_partial(s_rsrc, sgi);
         }
       }
       red_cx[sub][pc] = cx;
       red_s[sub][pc] = s;
     }
     __syncthreads();
-    if (t < kFinishCols && col0 + t < d.batch) {
+    if (t < kFinishCols && col0 + t < f.batch) {
+      const PckBatchCheckDesc& d = plan.desc[g];
       const double cx = (red_cx[0][t] + red_cx[1][t]) + (red_cx[2][t] + red_cx[3][t]);
       const double s = (red_s[0][t] + red_s[1][t]) + (red_s[2][t] + red_s[3][t]);
       const double ya = red_yabs[t];
-      const double s_bound = add_up_nonneg(s, static_cast<double>(d.n) * kSubnormalSlack);
+      const double s_bound = add_up_nonneg(s, static_cast<double>(f.n) * kSubnormalSlack);
       const double s_up = check::round_up_to_f32(mul_up_nonneg(s_bound, kSumSlack));
       const double rho = cx - red_ry[t];
       const double cabs_up = mul_up_nonneg(check::kOnePlusU32, s_up);
       const double eps = mul_up_nonneg(d.geps, add_up_nonneg(cabs_up, ya));
       const double tau =
           add_up_nonneg(add_up_nonneg(mul_up_nonneg(d.coef, s_up), eps), d.tau_floor);
-      const int64_t at = pair * d.batch + col0 + t;
+      const int64_t at = pair * f.batch + col0 + t;
       d.passed[at] = __builtin_isfinite(ya) && __builtin_isfinite(tau) && __builtin_fabs(rho) <= tau;
       d.rho[at] = rho;
       d.tau[at] = tau;
     }
     __syncthreads();  // the LDS sums are rewritten for the next check
-  }
+  } while (++k < f.checks);
 }
 
 // Fills the plan's counts; returns the workspace bytes, or -1 for an invalid descriptor.
@@ -440,13 +544,15 @@ int64_t make_plan(const PckBatchCheckDesc* descs, int count, Plan& plan) {
   int64_t tile_columns = 0;  // sum of pair tiles x column tiles x n
   for (int g = 0; g < count; ++g) {
     const PckBatchCheckDesc& d = descs[g];
-    if (d.num_blocks < 1 || d.checks < 1 || d.block < 4 || d.block % 4 != 0 || d.n < 8 ||
+    if (d.num_blocks < 1 || d.checks < 1 || d.block < 4 || d.block % 4 != 0 ||
+        d.block >= (int64_t{1} << 30) || d.n < 8 ||
         d.n % 8 != 0 || d.batch < 1 || !d.c || !d.a || !d.r || !d.X || !d.Y || !d.passed ||
         !d.rho || !d.tau || d.n > (1 << 20) || reinterpret_cast<uintptr_t>(d.X) % 16 != 0 ||
         reinterpret_cast<uintptr_t>(d.c) % 16 != 0 || reinterpret_cast<uintptr_t>(d.a) % 16 != 0 ||
         reinterpret_cast<uintptr_t>(d.Y) % 16 != 0 || reinterpret_cast<uintptr_t>(d.r) % 4 != 0 ||
         d.checks * d.num_blocks * d.n * 4 >= 0x80000000ll || d.batch * d.n * 2 >= 0x80000000ll ||
         d.num_blocks * ((d.batch + kFinishCols - 1) / kFinishCols) >= 0x80000000ll ||
+        d.num_blocks * d.block * kFinishCols * 4 >= 0x80000000ll ||  // one finish's outputs
         !(d.coef >= 0.0 && d.geps >= 0.0 && d.tau_floor >= 0.0) ||  // NaN fails too
         !__builtin_isfinite(d.coef + d.geps + d.tau_floor))
       return -1;
@@ -473,7 +579,40 @@ int64_t make_plan(const PckBatchCheckDesc* descs, int count, Plan& plan) {
     plan.finish[g + 1] =
         plan.finish[g] + d.num_blocks * ((d.batch + kFinishCols - 1) / kFinishCols);
     plan.slots[g + 1] = plan.slots[g] + pairs * d.batch * plan.segments[g];
+    PartialDesc& p = plan.part[g];
+    p.c = d.c;
+    p.a = d.a;
+    p.X = d.X;
+    p.slot = plan.slots[g];
+    p.start = static_cast<int32_t>(plan.start[g]);
+    p.segments = static_cast<int32_t>(plan.segments[g]);
+    p.pair_tiles = static_cast<int32_t>(plan.pair_tiles[g]);
+    p.pairs = static_cast<int32_t>(pairs);
+    p.num_blocks = static_cast<int32_t>(d.num_blocks);
+    p.n = static_cast<int32_t>(d.n);
+    p.batch = static_cast<int32_t>(d.batch);
+    p.unused = 0;
+    FinishDesc& f = plan.fin[g];
+    f.Y = d.Y;
+    f.r = d.r;
+    f.slot = plan.slots[g];
+    f.outs = pairs * d.batch;
+    f.start = static_cast<int32_t>(plan.finish[g]);
+    f.num_blocks = static_cast<int32_t>(d.num_blocks);
+    f.block = static_cast<int32_t>(d.block);
+    f.checks = static_cast<int32_t>(d.checks);
+    f.batch = static_cast<int32_t>(d.batch);
+    f.segments = static_cast<int32_t>(plan.segments[g]);
+    f.n = static_cast<int32_t>(d.n);
+    f.unused = 0;
   }
+  for (int g = 0; g < PCK_MAX_BATCH; ++g) {
+    const bool live = g < count && plan.start[g] <= INT32_MAX && plan.finish[g] <= INT32_MAX;
+    plan.part_first[g] = live ? static_cast<int32_t>(plan.start[g]) : INT32_MAX;
+    plan.fin_first[g] = live ? static_cast<int32_t>(plan.finish[g]) : INT32_MAX;
+  }
+  // one descriptor's partials are addressed with 32-bit byte offsets
+  if (plan.slots[count] * static_cast<int64_t>(sizeof(double)) >= 0x80000000ll) return -1;
   return 2 * plan.slots[count] * static_cast<int64_t>(sizeof(double));
 }
 
