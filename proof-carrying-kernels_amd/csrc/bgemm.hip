@@ -588,7 +588,9 @@ __global__ void __launch_bounds__(kThreads) bgemm_packed_kernel(PackedArgs a) {
   }
 }
 
-// Packs (rows, n) row-major into the step-pair layout above; kFp8: one byte per element.
+// Packs (rows, n) row-major into the step-pair layout above, one piece per lane; kFp8: one byte
+// per element.  For E4M3 weights (packed once, at load time) and for BF16 sources that are not
+// 16-byte aligned.
 template <bool kFp8>
 __global__ void __launch_bounds__(256) pack_kernel(const char* __restrict__ src,
                                                    char* __restrict__ dst, int64_t rows,
@@ -619,6 +621,36 @@ __global__ void __launch_bounds__(256) pack_kernel(const char* __restrict__ src,
     }
     reinterpret_cast<uint4*>(dst)[p] = v;
   }
+}
+
+// BF16 (rows, n) row-major into the step-pair layout through LDS (activations, per call): a
+// workgroup takes one tile's four step pairs (32 rows x 64 columns), reads them with one
+// coalesced 16-byte load per lane (eight lanes per row), and writes their 256 packed 16-byte
+// pieces contiguously, one per lane.  Rows past the end are zero.
+__global__ void __launch_bounds__(256) pack_bf16_kernel(const char* __restrict__ src,
+                                                        char* __restrict__ dst, int64_t rows,
+                                                        int64_t n) {
+  __shared__ uint2 stage[32][17];  // 32 rows x 128 bytes, one 8-byte pad per row
+  const int64_t pairs = n / (2 * kStep);
+  const int64_t quads = pairs / 4;  // n % 128 == 0
+  const int64_t tile = blockIdx.x / quads;
+  const int64_t quad = blockIdx.x % quads;
+  const int t = static_cast<int>(threadIdx.x);
+  {
+    const int r = t / 8, seg = t % 8;
+    const int64_t row = tile * 32 + r;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (row < rows) v = *reinterpret_cast<const uint4*>(src + (row * n + quad * 64 + seg * 8) * 2);
+    stage[r][2 * seg] = make_uint2(v.x, v.y);
+    stage[r][2 * seg + 1] = make_uint2(v.z, v.w);
+  }
+  __syncthreads();
+  // Lane L = 32 h + l of step pair pl: row l, columns 16 pl + 4 h .. + 3 and 16 pl + 8 + 4 h ..
+  const int pl = t / 64, L = t % 64, l = L & 31, h = L >> 5;
+  const uint2 lo = stage[l][4 * pl + h];
+  const uint2 hi = stage[l][4 * pl + 2 + h];
+  reinterpret_cast<uint4*>(dst)[(tile * pairs + quad * 4 + pl) * 64 + L] =
+      make_uint4(lo.x, lo.y, hi.x, hi.y);
 }
 
 template <bool kFp8, bool kVector>
@@ -767,11 +799,15 @@ extern "C" int pck_bgemm_pack(int kind, const void* src, void* dst, int64_t rows
   if (tiles * 32 * n * esz > 0xFFFFFFFFll / 2 || reinterpret_cast<uintptr_t>(src) % 8 != 0 ||
       reinterpret_cast<uintptr_t>(dst) % 16 != 0)
     return hipErrorInvalidValue;
-  const dim3 grid(static_cast<unsigned>((pieces + 255) / 256));
   auto s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>((pieces + 255) / 256));
   if (kind == 1) {
     hipLaunchKernelGGL((pack_kernel<true>), grid, dim3(256), 0, s, static_cast<const char*>(src),
                        static_cast<char*>(dst), rows, n, pieces);
+  } else if (reinterpret_cast<uintptr_t>(src) % 16 == 0) {
+    const dim3 tgrid(static_cast<unsigned>(tiles * (n / 64)));  // one tile's four pairs each
+    hipLaunchKernelGGL(pack_bf16_kernel, tgrid, dim3(256), 0, s, static_cast<const char*>(src),
+                       static_cast<char*>(dst), rows, n);
   } else {
     hipLaunchKernelGGL((pack_kernel<false>), grid, dim3(256), 0, s, static_cast<const char*>(src),
                        static_cast<char*>(dst), rows, n, pieces);

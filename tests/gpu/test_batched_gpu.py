@@ -281,3 +281,43 @@ def test_packed_route_validation_and_fallback() -> None:
     bw = pack_batched_weights(torch.zeros(4, 8, dtype=torch.bfloat16, device=DEV))
     with pytest.raises(RuntimeError, match="shape"):
         gemm_batched(bw, torch.zeros(2, 16, dtype=torch.bfloat16, device=DEV))
+
+
+def _packed_layout(bits: np.ndarray) -> np.ndarray:
+    """The step-pair layout of `pck_bgemm_pack` restated on the host from (rows, n) BF16 bit
+    patterns: tile t, pair p, lane L = 32 h + l holds row 32 t + l, columns 16 p + 4 h .. + 3
+    then 16 p + 8 + 4 h .. + 3; rows past the end are zero."""
+    rows, n = bits.shape
+    tiles, pairs = (rows + 31) // 32, n // 16
+    padded = np.zeros((tiles * 32, n), dtype=np.uint16)
+    padded[:rows] = bits
+    out = np.zeros((tiles, pairs, 64, 8), dtype=np.uint16)
+    for h in range(2):
+        lanes = slice(32 * h, 32 * h + 32)
+        for p in range(pairs):
+            block = padded.reshape(tiles, 32, n)
+            out[:, p, lanes, 0:4] = block[:, :, 16 * p + 4 * h : 16 * p + 4 * h + 4]
+            out[:, p, lanes, 4:8] = block[:, :, 16 * p + 8 + 4 * h : 16 * p + 12 + 4 * h]
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("rows,n", [(33, 384), (100, 1024), (128, 4096), (256, 14336)])
+def test_activation_pack_layout_aligned_and_8_byte_aligned(rows: int, n: int) -> None:
+    """Both BF16 pack routes (16-byte aligned sources go through LDS, 8-byte aligned ones piece
+    by piece) write exactly the documented layout, including the zero rows of a ragged tile."""
+    from pck.cuda._lib import check, lib, stream_handle
+
+    rng = np.random.default_rng(rows * 7 + n)
+    bits = rng.integers(0, 1 << 16, (rows, n), dtype=np.uint16)
+    want = _packed_layout(bits)
+    flat = torch.from_numpy(bits.view(np.int16).reshape(-1).copy()).to(DEV)
+    # the same rows at a 16-byte aligned address and at one 8 bytes past it
+    holder = torch.zeros(rows * n + 4, dtype=torch.int16, device=DEV)
+    holder[4:] = flat
+    for src in (flat, holder[4:]):
+        dst = torch.full((want.size,), 0x5555, dtype=torch.int16, device=DEV)
+        check(lib().pck_bgemm_pack(0, src.data_ptr(), dst.data_ptr(), rows, n,
+                                   stream_handle(torch.device(DEV))), "pack")  # fmt: skip
+        got = dst.cpu().numpy().view(np.uint16)
+        assert src.data_ptr() % 16 == (0 if src is flat else 8)
+        assert np.array_equal(got, want)
