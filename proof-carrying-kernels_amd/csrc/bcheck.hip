@@ -161,11 +161,10 @@ __global__ void __launch_bounds__(kThreads) partial_kernel(const Plan plan) {
   __shared__ double red[2][kWaves][kPairsWG][kColsWG + 1];  // [c.x, a.|x|][quarter][pair][col]
 
   const int item = static_cast<int>(blockIdx.x);  // the launch checks the grid is < 2^31
-  // The descriptor: every comparison at once, so its loads are not a chain of dependent ones;
-  // then its whole record in one round trip.
-  // Every value below is needed before the first operand load.  Empty asm statements that
-  // read them make the compiler request them together: the plan's own fields with the search
-  // bounds, then the descriptor's record, two round trips instead of one per use.
+  // The descriptor: every bound compared at once (not a chain of dependent loads), then its
+  // whole record.  Every value below is needed before the first operand load; empty asm
+  // statements that read them make the compiler request them together, the plan's own fields
+  // with the bounds and then the record: two round trips instead of one per use.
   double* const part_cx = plan.part_cx;
   double* const part_s = plan.part_s;
   const int seg_len = static_cast<int>(plan.seg_len);  // at most n rounded up to the quantum
@@ -221,8 +220,8 @@ __global__ void __launch_bounds__(kThreads) partial_kernel(const Plan plan) {
     const uint32_t at = static_cast<uint32_t>(st) * kStep;
     // A lane past the quarter's end sets the offset's top bit, which puts every load past its
     // buffer (below 2^31 bytes), so it reads zero.  The bit is opaque to the compiler (an empty
-    // asm), so the loads stay unconditional: a select between two offsets was compiled into
-    // branches, each load behind a wait for every load in flight.
+    // asm), so the loads stay unconditional: a select between two offsets compiles into
+    // branches, with each load behind a wait for every load in flight.
     uint32_t out = j_lane + st * kStep < j_hi ? 0u : check::kOutOfRange;
     __asm__("" : "+v"(out));
     Staged v;
