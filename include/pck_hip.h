@@ -264,7 +264,9 @@ typedef struct PckBatchCheckDesc {
  * and adds the segments in a fixed order) with a caller-allocated workspace of
  * pck_batch_check_workspace bytes (8-byte aligned); the library allocates nothing.  The
  * workspace is not shared between calls that overlap.  Needs n % 8 == 0, block % 4 == 0,
- * c, a, X, Y 16-byte and r 4-byte aligned, and coef, geps, tau_floor finite and >= 0;
+ * c, a, X, Y 16-byte and r 4-byte aligned, and coef, geps, tau_floor finite and >= 0; the
+ * kernels address with 32-bit byte offsets, so each output needs nb * b * 256 < 2^31 (fewer
+ * than 2^23 rows) and each of the workspace's two partial arrays stays below 2^31 bytes;
  * otherwise hipErrorInvalidValue before anything is enqueued. */
 int pck_batch_check_workspace(const PckBatchCheckDesc* descs, int count, int64_t* bytes);
 int pck_batch_check(const PckBatchCheckDesc* descs, int count, void* workspace,
