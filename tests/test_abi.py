@@ -135,3 +135,44 @@ def test_struct_layouts_match_the_header(tmp_path: Path) -> None:
             assert getattr(structs[struct], field).offset == int(value), key
         else:
             assert ctypes.sizeof(structs[key]) == int(value), key
+
+
+def _check_descs(shapes: list[tuple[int, int, int, int, int]], x_offset: int = 0) -> ctypes.Array:
+    """Descriptors (n, block, num_blocks, checks, batch) with placeholder device addresses: the
+    plan only validates and sizes them, it never dereferences a pointer."""
+    descs = (_lib.PckBatchCheckDesc * len(shapes))()
+    for i, (n, block, nb, checks, batch) in enumerate(shapes):
+        d = descs[i]
+        base = 0x10000000 * (i + 1)
+        d.c, d.a, d.r = base, base + 0x1000000, base + 0x2000000
+        d.X, d.Y = base + 0x3000000 + x_offset, base + 0x4000000
+        d.passed, d.rho, d.tau = base + 0x5000000, base + 0x6000000, base + 0x7000000
+        d.n, d.block, d.num_blocks, d.checks, d.batch = n, block, nb, checks, batch
+        d.coef, d.geps, d.tau_floor = 1.0, 1e-7, 0.0
+    return descs
+
+
+def _workspace(descs: ctypes.Array) -> tuple[int, int]:
+    need = ctypes.c_int64(-1)
+    err = _lib.lib().pck_batch_check_workspace(descs, len(descs), ctypes.byref(need))
+    return err, need.value
+
+
+def test_batch_check_plan_sizes_the_llama_layer() -> None:
+    """The Llama-3-8B layer at B = 256, b = 128, K = 1: 442,368 tile-columns over 512
+    workgroups gives 1024-column segments (4 for n = 4096, 14 for n = 14336), so the partials
+    hold 256 x (48 x 4 + 32 x 4 + 224 x 4 + 32 x 14) FP64 pairs: 6,815,744 bytes."""
+    layer = [(4096, 128, 48, 1, 256), (4096, 128, 32, 1, 256), (4096, 128, 224, 1, 256),
+             (14336, 128, 32, 1, 256)]  # fmt: skip
+    assert _workspace(_check_descs(layer)) == (0, 6_815_744)
+
+
+def test_batch_check_plan_rejects_what_32_bit_offsets_cannot_address() -> None:
+    # one finish workgroup reads 64 columns of nb * b rows: below 2^31 bytes passes
+    assert _workspace(_check_descs([(8, 128, 65535, 1, 16)]))[0] == 0
+    assert _workspace(_check_descs([(8, 128, 65536, 1, 16)]))[0] != 0
+    # each partial array (pairs x batch x segments FP64 values) stays below 2^31 bytes
+    assert _workspace(_check_descs([(8, 4, 1 << 14, 1, (1 << 14) - 64)]))[0] == 0
+    assert _workspace(_check_descs([(8, 4, 1 << 14, 1, 1 << 14)]))[0] != 0
+    # X must be 16-byte aligned
+    assert _workspace(_check_descs([(4096, 128, 32, 1, 128)], x_offset=8))[0] != 0
