@@ -152,11 +152,21 @@ __device__ __forceinline__ void check_pair(const PckCheckBatch& batch, int64_t i
         av[k] = a4[at];
         xv[k] = x4[at];
       }
+      // All kAhead quads are requested before the first is used (the scheduler would otherwise
+      // move loads next to their uses for occupancy, one round trip after another).
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int k = 0; k < kAhead; ++k) {
-        const bool in = q0 + static_cast<int64_t>(k) * kThreads < nq;
-        const float4 c = in ? cv[k] : make_float4(0.f, 0.f, 0.f, 0.f);
-        const uint2 xx = in ? xv[k] : make_uint2(0u, 0u);
+        // Columns past the row are zeroed by masking their bits with a word the compiler
+        // cannot see through (an empty asm): a select on the loaded value would be compiled
+        // into a branch around its load, followed by a wait for every load in flight.
+        uint32_t keep = q0 + static_cast<int64_t>(k) * kThreads < nq ? 0xFFFFFFFFu : 0u;
+        __asm__("" : "+v"(keep));
+        const float4 c = make_float4(__uint_as_float(__float_as_uint(cv[k].x) & keep),
+                                     __uint_as_float(__float_as_uint(cv[k].y) & keep),
+                                     __uint_as_float(__float_as_uint(cv[k].z) & keep),
+                                     __uint_as_float(__float_as_uint(cv[k].w) & keep));
+        const uint2 xx = make_uint2(xv[k].x & keep, xv[k].y & keep);
         column(cx[0], sa[0], c.x, bf16_lo(av[k].x), bf16_lo(xx.x));
         column(cx[1], sa[1], c.y, bf16_hi(av[k].x), bf16_hi(xx.x));
         column(cx[2], sa[2], c.z, bf16_lo(av[k].y), bf16_lo(xx.y));
