@@ -233,6 +233,26 @@ def test_tau_and_rho_against_exact_arithmetic() -> None:
     tau_and_rho_within_bounds(X, Xt, Wt, n, Fraction(1, 2**15))
 
 
+@pytest.mark.parametrize("n", [776, 1032])
+def test_steps_cut_by_the_row_end(n: int) -> None:
+    """n % 8 == 0 but n % 32 != 0: the last K step of a row is cut inside, so lanes of one step
+    are in range and the rest read zero through the offsets' out-of-range bit.  rho and tau
+    stay within their proven bounds of the exact values, and a planted sign flip is caught by
+    exactly the cells the CPU checker flags."""
+    m, B = 64, 18
+    print(f"batched check cut step n={n}", flush=True)
+    W, X, Wt, Xt = problem(m, n, B, seed=n)
+    tau_and_rho_within_bounds(X, Xt, Wt, n, Fraction(1, 2**15))
+    height = batched_height(n)
+    checker = GpuBlockedChecker(Wt, 32, height, checks=2, generator=torch.Generator().manual_seed(n))
+    Y = gemm_batched(Wt, Xt)
+    bad = Y.clone()
+    bad[5, 40] = -bad[5, 40]
+    gpu = checker.check_batched(Xt, bad).verdict.cpu().numpy()
+    np.testing.assert_array_equal(gpu, cpu_verdicts(W, X, bad.cpu().numpy(), checker, height))
+    assert gpu.sum() == gpu.size - 1 and not gpu[1, 5]
+
+
 def test_tau_never_below_exact_for_wide_and_subnormal_x() -> None:
     """X spanning 2^-133 (BF16 subnormal) to 2^40 in one row: the matrix-core step truncates the
     small products against the large ones and may flush subnormal products; tau must still be at
