@@ -5,7 +5,7 @@
  *
  * Operands are in lane order (no matrix layout is built in): for tile t < tiles and step
  * s < steps, lane l < 64 reads A and B at element [(t * steps + s) * 64 + l] (one FP64 value,
- * or 8 BF16 values given as their 16-bit patterns) and its accumulator registers at
+ * or 8 or 4 BF16 values given as their 16-bit patterns) and its accumulator registers at
  * [t * 64 + l] (4 FP64, 16 or 4 FP32 values); after the last step it writes its result
  * registers to D at the same place.  1 <= tiles <= 2^20 and 1 <= steps <= 64, else
  * hipErrorInvalidValue before anything is enqueued.  Returns a hipError_t. */
@@ -33,6 +33,12 @@ int pck_probe_mfma_bf16(const uint16_t* a, const uint16_t* b, const float* c, fl
 /* Chains of v_mfma_f32_16x16x32_bf16: a, b as above, c, d (tiles * 64 * 4) floats. */
 int pck_probe_mfma_bf16_16x16(const uint16_t* a, const uint16_t* b, const float* c, float* d,
                               int64_t tiles, int steps, void* stream);
+
+/* Chains of v_mfma_f32_32x32x8_bf16 (the batched product's instruction): a, b (tiles * steps *
+ * 64 * 4) BF16 patterns, 4 per lane (lane l + 32 h holds row / column l, K-slots 4h .. 4h + 3),
+ * c, d (tiles * 64 * 16) floats. */
+int pck_probe_mfma_bf16_k8(const uint16_t* a, const uint16_t* b, const float* c, float* d,
+                           int64_t tiles, int steps, void* stream);
 
 #ifdef __cplusplus
 }

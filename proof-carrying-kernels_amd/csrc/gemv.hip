@@ -23,8 +23,10 @@
 // chain accumulator starts at -0.0, the additive identity of IEEE round-to-nearest, so
 // "-0 + p0" equals "start from p0" bit for bit, signed zero included.
 //
-// The naive kernel (reference gemv_kernel.cu:27-55, model src/pck/gemv.py:14-57) keeps the
-// reference's shape: one workgroup per row, a contiguous chunk per lane, an LDS pair tree.
+// The naive tree (reference model src/pck/gemv.py:14-57) fixes a different order: virtual lane
+// t sums the contiguous chunk [t c, (t + 1) c) of a row, then neighbour pairs combine level by
+// level.  Its kernel maps the levels of stride below 64 onto DPP / permlane moves inside a wave
+// and meets only the wave sums in LDS (gemv_naive_kernel below).
 
 #include <hip/hip_runtime.h>
 
@@ -393,28 +395,89 @@ __global__ void __launch_bounds__(kGroupThreads)
   gemv_rows<T, R, U, kFp8, kVector, kPad, kNt, true>(batch, group - ride_groups);
 }
 
-// Naive tree: one workgroup of `threads` lanes per row (reference gemv_kernel.cu:27-55).
+// Naive tree (order of the reference model src/pck/gemv.py:14-57): `threads` = T virtual lanes
+// per row, lane t owning the contiguous chunk [t c, (t + 1) c), c = ceil(n / T), summed in
+// column order from its first product (columns past n add +0), then the T chain sums combined
+// by neighbour pairs, stride 1, 2, 4, ...: a[t] += a[t + s] for t a multiple of 2s.
+//
+// One workgroup of max(T, 64) lanes per row, lane t of the workgroup being virtual lane t (lanes
+// t >= T, present only when T < 64, own chunks wholly past n and feed no level below T).  The
+// levels of stride 1 .. 32 run inside each wave: every lane adds the value of its partner lane
+// t + s, moved by DPP (quad permutes for 1 and 2, row rotations for 4 and 8), permlane16_swap
+// (16) or a read of lane 32 (32); the lanes that matter at a level read only lanes that
+// mattered at the level before, so lane 0 ends with the wave's subtree.  The levels of stride 64
+// and up combine the T / 64 wave sums, which meet in LDS behind one barrier, in the same pair
+// order.  kVector: 16-byte loads of W and x (c and n multiples of 8, aligned pointers), every
+// vector wholly before or wholly past n.
+template <bool kVector>
 __global__ void __launch_bounds__(1024)
     gemv_naive_kernel(const uint16_t* __restrict__ W, const uint16_t* __restrict__ x,
-                      float* __restrict__ y, int64_t n, int64_t chunk) {
-  extern __shared__ float partial[];
+                      float* __restrict__ y, int64_t n, int64_t chunk, int threads) {
+  __shared__ float wave_sum[1024 / kWave];
   const int t = static_cast<int>(threadIdx.x);
-  const uint16_t* w_row = W + static_cast<int64_t>(blockIdx.x) * n;
-  const int64_t begin = t * chunk;
-  auto product = [&](int64_t j) {
-    const float wv = __uint_as_float(static_cast<uint32_t>(w_row[j]) << 16);
-    const float xv = __uint_as_float(static_cast<uint32_t>(x[j]) << 16);
-    return wv * xv;
-  };
-  float acc = begin < n ? product(begin) : 0.0f;
-  for (int64_t j = begin + 1; j < begin + chunk; ++j) acc = acc + (j < n ? product(j) : 0.0f);
-  partial[t] = acc;
-  __syncthreads();
-  for (int stride = 1; stride < static_cast<int>(blockDim.x); stride *= 2) {
-    if (t % (2 * stride) == 0) partial[t] = partial[t] + partial[t + stride];
-    __syncthreads();
+  const int lane = t & (kWave - 1);
+  const uint16_t* row = W + static_cast<int64_t>(blockIdx.x) * n;
+  const int64_t first = static_cast<int64_t>(t) * chunk;
+
+  float acc = 0.0f;
+  if constexpr (kVector) {
+    for (int64_t v = 0; v < chunk; v += 8) {
+      const int64_t col = first + v;
+      uint4 wv = make_uint4(0, 0, 0, 0), xv = make_uint4(0, 0, 0, 0);  // past n: +0 products
+      if (col < n) {
+        wv = *reinterpret_cast<const uint4*>(row + col);
+        xv = *reinterpret_cast<const uint4*>(x + col);
+      }
+      const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+      const uint32_t xd[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float p0 = bf16_lo(wd[k]) * bf16_lo(xd[k]);
+        const float p1 = bf16_hi(wd[k]) * bf16_hi(xd[k]);
+        acc = (v == 0 && k == 0) ? p0 : acc + p0;
+        acc = acc + p1;
+      }
+    }
+  } else {
+    for (int64_t j = first; j < first + chunk; ++j) {
+      float p = 0.0f;
+      if (j < n) p = __uint_as_float(static_cast<uint32_t>(row[j]) << 16) *
+                     __uint_as_float(static_cast<uint32_t>(x[j]) << 16);
+      acc = j == first ? p : acc + p;
+    }
   }
-  if (t == 0) y[blockIdx.x] = partial[0];
+
+  // Levels inside the wave (uniform bounds: `threads` is the same for every lane).
+  if (threads > 1) acc = acc + dpp_move<0xB1>(acc);   // stride 1: quad_perm [1,0,3,2]
+  if (threads > 2) acc = acc + dpp_move<0x4E>(acc);   // stride 2: quad_perm [2,3,0,1]
+  if (threads > 4) acc = acc + dpp_move<0x12C>(acc);  // stride 4: row_ror:12, lane i <- i + 4
+  if (threads > 8) acc = acc + dpp_move<0x128>(acc);  // stride 8: row_ror:8, lane i <- i + 8
+  if (threads > 16) {                                  // stride 16: lanes 0-15 <- 16-31
+    const auto swapped =
+        __builtin_amdgcn_permlane16_swap(__float_as_int(acc), __float_as_int(acc), false, false);
+    acc = acc + __int_as_float(swapped[1]);
+  }
+  if (threads > 32) acc = lane_value(acc, 0) + lane_value(acc, 32);  // stride 32
+
+  if (threads <= kWave) {
+    if (t == 0) y[blockIdx.x] = acc;
+    return;
+  }
+  // Levels across waves: wave w's subtree is a[64 w]; pairs of stride 64, 128, ...
+  if (lane == 0) wave_sum[t / kWave] = acc;
+  __syncthreads();
+  if (t == 0) {
+    const int waves = threads / kWave;
+    float a[1024 / kWave];
+#pragma unroll
+    for (int w = 0; w < 1024 / kWave; ++w) a[w] = w < waves ? wave_sum[w] : 0.0f;
+#pragma unroll
+    for (int s = 1; s < 1024 / kWave; s *= 2)
+#pragma unroll
+      for (int w = 0; w + s < 1024 / kWave; w += 2 * s)
+        if (s < waves) a[w] = a[w] + a[w + s];
+    y[blockIdx.x] = a[0];
+  }
 }
 
 // Launch shape of the coalesced kernel: rows per wave slot, vector positions loaded ahead and
@@ -702,14 +765,21 @@ int pck_gemv_group_fp8_scaled(const PckGemv* gemvs, const float* const* scales,
 int pck_gemv_bf16_naive(const void* W, const void* x, float* y, int64_t m, int64_t n, int threads,
                         void* stream) {
   if (threads < 1 || threads > 1024 || (threads & (threads - 1)) != 0) return hipErrorInvalidValue;
-  if (m < 0 || m > 0x7FFFFFFF || m * threads > 0xFFFFFFFFll) return hipErrorInvalidValue;
+  const int64_t lanes = threads < 64 ? 64 : threads;  // workgroup size of the launch
+  if (m < 0 || m > 0x7FFFFFFF || m * lanes > 0xFFFFFFFFll) return hipErrorInvalidValue;
   if (m == 0) return hipSuccess;
   if (n < 1 || !W || !x || !y) return hipErrorInvalidValue;
   const int64_t chunk = (n + threads - 1) / threads;
-  pck::gemv_naive_kernel<<<dim3(static_cast<unsigned>(m)), dim3(threads),
-                           static_cast<size_t>(threads) * sizeof(float),
-                           static_cast<hipStream_t>(stream)>>>(
-      static_cast<const uint16_t*>(W), static_cast<const uint16_t*>(x), y, n, chunk);
+  const bool vector = chunk % 8 == 0 && n % 8 == 0 && reinterpret_cast<uintptr_t>(W) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(x) % 16 == 0;
+  const dim3 grid(static_cast<unsigned>(m)), group(static_cast<unsigned>(lanes));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const auto* w16 = static_cast<const uint16_t*>(W);
+  const auto* x16 = static_cast<const uint16_t*>(x);
+  if (vector)
+    pck::gemv_naive_kernel<true><<<grid, group, 0, s>>>(w16, x16, y, n, chunk, threads);
+  else
+    pck::gemv_naive_kernel<false><<<grid, group, 0, s>>>(w16, x16, y, n, chunk, threads);
   return hipGetLastError();
 }
 

@@ -5,12 +5,14 @@
 //   pck_probe_expf            y = expf(x), the FP32 exponential the membership and sampling
 //                             kernels call (same header, same flags, same code);
 //   pck_probe_mfma_f64        v_mfma_f64_16x16x4_f64 chains, as the batched checker runs c . x;
-//   pck_probe_mfma_bf16       v_mfma_f32_32x32x16_bf16 chains (the batched product's step);
+//   pck_probe_mfma_bf16       v_mfma_f32_32x32x16_bf16 chains;
+//   pck_probe_mfma_bf16_k8    v_mfma_f32_32x32x8_bf16 chains (the batched product's step: one
+//                             group of 8 K-slots split over the two lane halves, 4 per lane);
 //   pck_probe_mfma_bf16_16x16 v_mfma_f32_16x16x32_bf16 chains (the batched checker's a . |x|).
 //
 // Operands are passed in lane order, so the probes embed no matrix layout: tile t, step s,
-// lane l reads its A and B operands at [(t * steps + s) * 64 + l] (8 BF16 values or one FP64
-// value each) and its accumulator registers at [t * 64 + l] (16, 4 or 4 values), and writes
+// lane l reads its A and B operands at [(t * steps + s) * 64 + l] (8 or 4 BF16 values or one
+// FP64 value each) and its accumulator registers at [t * 64 + l] (16, 4 or 4 values), and writes
 // the result registers after the last step in the same place of D.  One wave per tile; every
 // tile index below `tiles`, so each access stays inside buffers of the documented sizes.
 
@@ -25,6 +27,8 @@ namespace {
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kWave = 64;
 
@@ -72,6 +76,23 @@ __global__ void __launch_bounds__(kWave) mfma_bf16_kernel(const uint16_t* a, con
   for (int v = 0; v < kRegs; ++v) d[(t * kWave + l) * kRegs + v] = acc[v];
 }
 
+// Four BF16 operands per lane (8 bytes): v_mfma_f32_32x32x8_bf16, the instruction the batched
+// product issues.
+__global__ void __launch_bounds__(kWave) mfma_bf16_k8_kernel(const uint16_t* a, const uint16_t* b,
+                                                             const float* c, float* d, int steps) {
+  const int64_t t = blockIdx.x;
+  const int l = static_cast<int>(threadIdx.x);
+  f32x16 acc;
+  for (int v = 0; v < 16; ++v) acc[v] = c[(t * kWave + l) * 16 + v];
+  for (int s = 0; s < steps; ++s) {
+    const int64_t o = ((t * steps + s) * kWave + l) * 4;
+    const s16x4 av = *reinterpret_cast<const s16x4*>(a + o);
+    const s16x4 bv = *reinterpret_cast<const s16x4*>(b + o);
+    acc = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(av, bv, acc, 0, 0, 0);
+  }
+  for (int v = 0; v < 16; ++v) d[(t * kWave + l) * 16 + v] = acc[v];
+}
+
 bool tiles_ok(int64_t tiles, int steps) {
   return tiles >= 1 && tiles <= (1 << 20) && steps >= 1 && steps <= 64;
 }
@@ -107,6 +128,14 @@ extern "C" int pck_probe_mfma_bf16_16x16(const uint16_t* a, const uint16_t* b, c
                                          float* d, int64_t tiles, int steps, void* stream) {
   if (!tiles_ok(tiles, steps) || !a || !b || !c || !d) return hipErrorInvalidValue;
   mfma_bf16_kernel<4><<<dim3(static_cast<unsigned>(tiles)), dim3(kWave), 0,
+                        static_cast<hipStream_t>(stream)>>>(a, b, c, d, steps);
+  return hipGetLastError();
+}
+
+extern "C" int pck_probe_mfma_bf16_k8(const uint16_t* a, const uint16_t* b, const float* c,
+                                      float* d, int64_t tiles, int steps, void* stream) {
+  if (!tiles_ok(tiles, steps) || !a || !b || !c || !d) return hipErrorInvalidValue;
+  mfma_bf16_k8_kernel<<<dim3(static_cast<unsigned>(tiles)), dim3(kWave), 0,
                         static_cast<hipStream_t>(stream)>>>(a, b, c, d, steps);
   return hipGetLastError();
 }

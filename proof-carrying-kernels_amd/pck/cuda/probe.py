@@ -3,9 +3,10 @@ library's flags; header include/pck_probe.h).  Tests call these on the GPU and c
 results with exact host arithmetic; nothing in the product path uses them.
 
 Operands are in lane order: for a chain of ``steps`` matrix-core steps over ``tiles`` tiles,
-``a`` and ``b`` have shape (tiles, steps, 64) (FP64) or (tiles, steps, 64, 8) (BF16), the
-accumulator ``c`` (tiles, 64, R) with R result registers per lane (4 for FP64 16x16x4, 16 for
-BF16 32x32x16, 4 for BF16 16x16x32), and the result has the shape of ``c``.
+``a`` and ``b`` have shape (tiles, steps, 64) (FP64), (tiles, steps, 64, 8) (BF16, 16 K-slots
+per step) or (tiles, steps, 64, 4) (BF16 32x32x8), the accumulator ``c`` (tiles, 64, R) with R
+result registers per lane (4 for FP64 16x16x4, 16 for BF16 32x32x16 and 32x32x8, 4 for BF16
+16x16x32), and the result has the shape of ``c``.
 """
 
 from __future__ import annotations
@@ -25,6 +26,7 @@ SIGNATURES = {
     "pck_probe_mfma_f64": [_p, _p, _p, _p, _i64, _int, _p],
     "pck_probe_mfma_bf16": [_p, _p, _p, _p, _i64, _int, _p],
     "pck_probe_mfma_bf16_16x16": [_p, _p, _p, _p, _i64, _int, _p],
+    "pck_probe_mfma_bf16_k8": [_p, _p, _p, _p, _i64, _int, _p],
 }
 _handle: ctypes.CDLL | None = None
 
@@ -97,4 +99,12 @@ def mfma_bf16_16x16(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor) -> torch.
     """Chains of v_mfma_f32_16x16x32_bf16 (a, b: (tiles, steps, 64, 8) BF16; c: (tiles, 64, 4)
     FP32)."""
     return _chain("pck_probe_mfma_bf16_16x16", a.view(torch.int16), b.view(torch.int16), c, 8, 4,
+                  torch.int16)  # fmt: skip
+
+
+def mfma_bf16_k8(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor) -> torch.Tensor:
+    """Chains of v_mfma_f32_32x32x8_bf16, the batched product's instruction (a, b: (tiles,
+    steps, 64, 4) BF16, lane l + 32 h holding row / column l and K-slots 4h .. 4h + 3;
+    c: (tiles, 64, 16) FP32)."""
+    return _chain("pck_probe_mfma_bf16_k8", a.view(torch.int16), b.view(torch.int16), c, 4, 16,
                   torch.int16)  # fmt: skip

@@ -2,17 +2,17 @@
 
 MI355X keeps a 256 MB Infinity Cache (MALL) behind its per-XCD L2s, and every Llama-3-8B
 projection fits in it, so a flush of 2 x L2 (the reference's) would report MALL bandwidth as
-HBM bandwidth.  `ColdL2Timer` keeps the reference's name and interface but overwrites at least
+HBM bandwidth.  `ColdL2Timer` keeps the reference's name and interface and scrubs
 2 x (L2 + MALL) before every rep.
 """
 
 from __future__ import annotations
 
 import re
-import statistics
 from collections.abc import Callable
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 MALL_BYTES = 256 << 20
@@ -38,34 +38,58 @@ class Timing:
 
 
 class ColdL2Timer:
-    """Times a GPU function with events, flushing L2 and the MALL before every rep."""
+    """Times a GPU function rep by rep with events on the current stream, each rep starting
+    from caches that hold none of its data (the reference's `ColdL2Timer` interface:
+    ``ColdL2Timer(warmup, reps)(fn) -> Timing``).
+
+    Before every rep a fill kernel writes a fresh byte value over a scrub buffer of
+    2 x (L2 + MALL) bytes, so every line the previous rep left in L2 or the MALL has been
+    replaced by the time the rep starts.  The reps are enqueued back to back and read after one
+    synchronisation; the summary is the 10th, 50th and 90th percentiles of the rep times
+    (linear interpolation between order statistics).
+    """
 
     def __init__(self, warmup: int, reps: int) -> None:
-        self.flush = torch.empty(2 * cache_bytes(), dtype=torch.uint8, device="cuda")
+        if warmup < 0 or reps < 1:
+            raise ValueError(f"need warmup >= 0 and reps >= 1, got {warmup}, {reps}")
         self.warmup, self.reps = warmup, reps
+        self._scrub = torch.empty(2 * cache_bytes(), dtype=torch.uint8, device="cuda")
+        self._fill = 0
+
+    @property
+    def flush(self) -> torch.Tensor:
+        """The scrub buffer written before every rep."""
+        return self._scrub
+
+    def _scrub_caches(self) -> None:
+        self._fill = (self._fill + 1) % 256
+        self._scrub.fill_(self._fill)
 
     def __call__(self, fn: Callable[[], object]) -> Timing:
         for _ in range(self.warmup):
             fn()
-        starts = [torch.cuda.Event(enable_timing=True) for _ in range(self.reps)]
-        ends = [torch.cuda.Event(enable_timing=True) for _ in range(self.reps)]
-        for start, end in zip(starts, ends, strict=True):
-            self.flush.zero_()
-            start.record()
+        marks = [torch.cuda.Event(enable_timing=True) for _ in range(2 * self.reps)]
+        for rep in range(self.reps):
+            self._scrub_caches()
+            marks[2 * rep].record()
             fn()
-            end.record()
-        torch.cuda.synchronize()
-        times = sorted(float(s.elapsed_time(e)) for s, e in zip(starts, ends, strict=True))
-        deciles = statistics.quantiles(times, n=10)
-        return Timing(statistics.median(times), deciles[0], deciles[-1])
+            marks[2 * rep + 1].record()
+        marks[-1].synchronize()
+        ms = np.array([marks[2 * r].elapsed_time(marks[2 * r + 1]) for r in range(self.reps)])
+        p10, p50, p90 = np.percentile(ms, [10.0, 50.0, 90.0])
+        return Timing(median_ms=float(p50), p10_ms=float(p10), p90_ms=float(p90))
 
 
 def copy_bandwidth_gbps(timer: ColdL2Timer, nbytes: int = 1 << 30) -> float:
-    """Device-to-device copy bandwidth (read + write) (reference `timing.py:50-55`)."""
-    src = torch.empty(nbytes // 2, dtype=torch.uint8, device="cuda")
-    dst = torch.empty_like(src)
+    """Device-to-device copy bandwidth, a practical DRAM ceiling (the reference's
+    `copy_bandwidth_gbps` figure): one ``nbytes`` buffer whose first half is copied onto its
+    second half, so every rep reads nbytes / 2 and writes nbytes / 2; bytes moved per second of
+    the median rep."""
+    half = nbytes // 2
+    buf = torch.empty(2 * half, dtype=torch.uint8, device="cuda")
+    src, dst = buf[:half], buf[half:]
     t = timer(lambda: dst.copy_(src))
-    return float(2 * src.numel() / (t.median_ms / 1e3) / 1e9)
+    return float(2 * half / (t.median_ms * 1e-3) / 1e9)
 
 
 READ_CHUNK = 64 << 10  # bytes per workgroup of the read stream (fastest measured on MI355X)

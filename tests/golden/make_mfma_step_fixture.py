@@ -16,6 +16,12 @@ Run on an MI355X from the repository root:
    halves populated with a zero accumulator, and chains of three steps from a nonzero
    accumulator.  The CPU tests check them against exact sums and a bound, and record that
    they do not follow the one-group rule extended to two groups.
+3. The same populated group through v_mfma_f32_32x32x8_bf16, the instruction the batched
+   product issues (K8_Y_diag, K8_Y_block): its one group of 8 K-slots spans both lane halves,
+   lane l + 32 h holding row l's slots 4h .. 4h + 3, zero accumulator.  And random steps of
+   that instruction in lane order (k8_full_*): every lane populated, zero accumulator, the
+   product's own operand kinds (N(0, 0.02) BF16 weights against N(0, 1) activations) and
+   wide-range ones.
 """
 
 from __future__ import annotations
@@ -99,6 +105,17 @@ def tile_operands(W: np.ndarray, X: np.ndarray, ti: int, tb: int) -> tuple[np.nd
     return a, b
 
 
+def tile_operands_k8(W: np.ndarray, X: np.ndarray, ti: int, tb: int) -> tuple[np.ndarray, np.ndarray]:
+    """(a, b) lane operands of one v_mfma_f32_32x32x8_bf16 step: lane l + 32 h holds K-slots
+    4h .. 4h + 3 of W row 32 ti + l and of X row 32 tb + l."""
+    a = np.zeros((64, 4), np.float32)
+    b = np.zeros((64, 4), np.float32)
+    for h in range(2):
+        a[32 * h : 32 * h + 32] = W[32 * ti : 32 * ti + 32, 4 * h : 4 * h + 4]
+        b[32 * h : 32 * h + 32] = X[32 * tb : 32 * tb + 32, 4 * h : 4 * h + 4]
+    return a, b
+
+
 def output_index(lane: np.ndarray, reg: int) -> tuple[np.ndarray, np.ndarray]:
     """(row of A, column of B) of result register `reg` in lane `lane` of a 32 x 32 tile."""
     return 8 * (reg // 4) + 4 * (lane // 32) + reg % 4, lane % 32
@@ -116,6 +133,13 @@ def chains(seed: int = 9) -> dict[str, np.ndarray]:
         out[name + "_b"] = bf16(rng.standard_normal((tiles, steps, 64, 8)) * scale[1])
         acc = rng.standard_normal((tiles, 64, 16)) * np.exp2(rng.integers(-8, 9, (tiles, 64, 16)))
         out[name + "_c"] = (acc * (name == "chain")).astype(np.float32)
+    tiles = 8
+    wide = np.exp2(rng.integers(-20, 21, (2, tiles, 1, 64, 4)))
+    a = rng.standard_normal((tiles, 1, 64, 4)) * np.where(np.arange(tiles)[:, None, None, None] < 4, 0.02, wide[0])
+    b = rng.standard_normal((tiles, 1, 64, 4)) * np.where(np.arange(tiles)[:, None, None, None] < 4, 1.0, wide[1])
+    out["k8_full_a"] = bf16(a)
+    out["k8_full_b"] = bf16(b)
+    out["k8_full_c"] = np.zeros((tiles, 64, 16), np.float32)
     return out
 
 
@@ -143,10 +167,24 @@ def main() -> None:
         for reg in range(16):
             i, j = output_index(lanes, reg)
             Y[32 * tb + j, 32 * ti + i] = d[k, :, reg]
+    ops8 = [tile_operands_k8(W, X, ti, tb) for ti, tb in tiles]
+    a8 = np.stack([o[0] for o in ops8])[:, None]
+    b8 = np.stack([o[1] for o in ops8])[:, None]
+    d8 = probe.mfma_bf16_k8(dev(a8), dev(b8), torch.zeros((len(tiles), 64, 16), device="cuda")).cpu().numpy()
+    Y8 = np.full_like(Y, np.nan)
+    for k, (ti, tb) in enumerate(tiles):
+        for reg in range(16):
+            i, j = output_index(lanes, reg)
+            Y8[32 * tb + j, 32 * ti + i] = d8[k, :, reg]
     extra = chains()
     for name in ("full", "chain"):
         extra[name + "_d"] = probe.mfma_bf16(dev(extra[name + "_a"]), dev(extra[name + "_b"]),
                                              torch.from_numpy(extra[name + "_c"]).cuda()).cpu().numpy()  # fmt: skip
+    extra["k8_full_d"] = probe.mfma_bf16_k8(dev(extra["k8_full_a"]), dev(extra["k8_full_b"]),
+                                            torch.from_numpy(extra["k8_full_c"]).cuda()).cpu().numpy()  # fmt: skip
+    extra["K8_Y_diag"] = np.diagonal(Y8).copy()
+    extra["K8_Y_block"] = Y8[:, :BLOCK].copy()
+    assert not np.isnan(extra["K8_Y_diag"]).any() and not np.isnan(extra["K8_Y_block"]).any()
     torch.cuda.synchronize()
     save(args.out, W, X, Y, torch.cuda.get_device_name(), extra)
 

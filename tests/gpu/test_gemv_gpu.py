@@ -16,7 +16,7 @@ from hypothesis import strategies as st
 from numpy.typing import NDArray
 
 from oracle.checker import BlockedChecker
-from oracle.cmodel import gemv_coalesced_c
+from oracle.cmodel import gemv_coalesced_c, gemv_naive_c
 from oracle.gemv import e4m3_values, emulate_gemv, emulate_gemv_coalesced, reference_gemv
 from pck.cuda import gemv_coalesced, gemv_fp8, gemv_group, gemv_naive, quantize_fp8
 from pck.cuda._lib import lib
@@ -86,10 +86,33 @@ def test_bit_exact_with_model(kernel: Kernel, m: int, n: int, threads: int) -> N
     assert_bits(run(kernel, W, x, threads), kernel.model(W, x, threads))
 
 
-@pytest.mark.parametrize("threads", [1, 2, 4, 16])
+@pytest.mark.parametrize("threads", [1, 2, 4, 8, 16])
 def test_naive_small_thread_counts(threads: int) -> None:
     W, x = random_problem(9, 77, seed=threads)
     assert_bits(run(KERNELS[0], W, x, threads), emulate_gemv(W, x, threads))
+
+
+# (m, n, threads): chunks of whole 16-byte vectors (every level inside one wave, across 2, 4,
+# 8 and 16 waves) and chunks that are not (element loads), with n ragged or not.
+NAIVE_PATHS = [(6, 256, 8), (6, 2048, 32), (5, 512, 64), (4, 1024, 128), (3, 8192, 1024),
+               (7, 8200, 1024), (9, 4104, 64), (4, 4096, 512), (2, 65, 64)]  # fmt: skip
+
+
+@pytest.mark.parametrize(("m", "n", "threads"), NAIVE_PATHS)
+def test_naive_vector_and_element_paths(m: int, n: int, threads: int) -> None:
+    W, x = random_problem(m, n, seed=n + threads)
+    assert_bits(run(KERNELS[0], W, x, threads), emulate_gemv(W, x, threads))
+
+
+@pytest.mark.parametrize(("m", "n"), [(1024, 4096), (4096, 14336)])
+def test_naive_llama_shapes_bit_exact(m: int, n: int) -> None:
+    """The naive tree at T = 256 on decode shapes (chunks of 16 and 56 columns) against the
+    C model of the same order."""
+    g = torch.Generator().manual_seed(1)
+    W = (torch.randn(m, n, generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(n, generator=g).to(torch.bfloat16)
+    y = gemv_naive(W.cuda(), x.cuda(), 256).cpu().numpy()
+    assert_bits(y, gemv_naive_c(W.float().numpy(), x.float().numpy(), 256))
 
 
 @kernels
