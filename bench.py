@@ -21,13 +21,19 @@ are replayed in alternating rounds, max(7, steps / 32) rounds whatever --steps i
 The headline `value` is the carried mode at b = 128.  A B = 1 fault campaign plants the
 reference's shortcuts (dropped tail, BF16 accumulator / partials / output) and per-block
 exponent and sign flips in every output of one layer and reports caught outputs and false
-alarms for the bank and row-sum checks at b = 128 and 256.
+alarms for the bank and row-sum checks at b = 128 and 256, K = 1, plus two faults planted
+inside the producing in-pass launch.  The detection campaign of `campaign.py` (the reference's
+protocol at K = 8: >= 10^7 honest block checks per kernel and block size, per-bit flip rates,
+every shortcut at batch 1 and on the batched down projection) runs in the default section too.
 
 Printed: one compact JSON line on stdout (the contract line) and the full per-section figures
 as one `[bench detail]` JSON line on stderr.  The contract line holds:
   value          GEMV algorithmic bytes per step / time per replayed step, checker included
   checker_overhead_pct, fp8_checker_overhead_pct   every mode above against gemv_only
-  faults_b1      the campaign's caught outputs and false alarms
+  faults_b1      the K = 1 campaign's caught outputs, false alarms and each escape's
+                 |rho| / tau; `inlaunch`: faults planted inside the producing launch
+  detection_k8   the K = 8 campaign: alarms and the largest |rho| / tau per activation family,
+                 per-bit flip detection rates, caught shortcut outputs with every escape
   membership     the top-k / top-p membership check, 256 x 151,936 logits
   vllm_plugin    the plugin wrapper's cost per step at the same size, beside the check alone
   batched        B = 128 and 256: products, checker overhead, caught faulty columns (with the
@@ -47,7 +53,7 @@ each GEMV launch's bytes (size_matched_read_us; pct_of_size_matched_read is thei
 layer's time).
 
 Run: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--quick]
-                     [--section all|b1|templates|members|batched]
+                     [--section all|b1|templates|members|batched|campaign]
 """
 
 from __future__ import annotations
@@ -413,110 +419,88 @@ def timed(layers, steps: int, warmup: int, with_check: bool, per_kernel: bool): 
     return start.elapsed_time(end) / steps, per_launch
 
 
-def naive_shortcut(W, x, acc_bf16: bool = False, partial_bf16: bool = False):  # type: ignore[no-untyped-def]
-    """y = W x in the naive kernel's order (T = 256 lanes, lane t sums the contiguous chunk
-    [t c, (t + 1) c), then neighbour pairs) with one of the reference's planted shortcuts
-    (src/pck/gemv.py:14-57): the running sum rounded to BF16 after every add, or each lane's
-    chain sum rounded to BF16.  Torch ops on the GPU: the bench's fault generator."""
-    import torch
-
-    m, n = W.shape
-    lanes = 256
-    chunk = -(-n // lanes)
-    p = torch.zeros(m, lanes * chunk, device=W.device)
-    p[:, :n] = W.float() * x.float()
-    p = p.view(m, lanes, chunk)
-    acc = p[:, :, 0].clone()
-    for j in range(1, chunk):
-        acc = acc + p[:, :, j]
-        if acc_bf16:
-            acc = acc.bfloat16().float()
-    if partial_bf16:
-        acc = acc.bfloat16().float()
-    while acc.size(1) > 1:
-        acc = acc[:, 0::2] + acc[:, 1::2]
-    return acc[:, 0].contiguous()
-
-
-def planted_faults(W, x, y, gen):  # type: ignore[no-untyped-def]
-    """The reference campaign's faults for one GEMV output (harness/campaign.py:56-135):
-    a dropped reduction tail of 4 columns (the honest kernel on W with them zeroed), the BF16
-    accumulator and BF16 partials shortcuts, the BF16-rounded output, and one flip per block of
-    a random exponent bit (23-30) or of the sign bit of a random output."""
-    import torch
-
-    from pck.cuda import gemv_group
-
-    Wz = W.clone()
-    Wz.view(torch.uint8 if W.element_size() == 1 else torch.int16)[:, -4:] = 0
-    out = {
-        "drop_tail_4": gemv_group([(Wz, x)], THREADS)[0],
-        "bf16_accumulator": naive_shortcut(W, x, acc_bf16=True),
-        "bf16_partials": naive_shortcut(W, x, partial_bf16=True),
-        "bf16_output": y.bfloat16().float(),
-    }
-    blocks = y.numel() // BLOCK
-    base = torch.arange(0, y.numel(), BLOCK, device=y.device)
-    for kind, lo, hi in (("exponent_flip", 23, 31), ("sign_flip", 31, 32)):
-        rows = base + torch.randint(0, BLOCK, (blocks,), generator=gen).to(y.device)
-        bit = torch.randint(lo, hi, (blocks,), generator=gen).to(y.device)
-        z = y.clone()
-        zi = z.view(torch.int32)
-        zi[rows] ^= torch.bitwise_left_shift(torch.ones_like(bit, dtype=torch.int32), bit.int())
-        out[kind] = z
-    return out
-
-
 def fault_campaign_b1(layer, seed: int) -> dict:  # type: ignore[no-untyped-def]
     """BASELINE config 4, reference-parity reading (batch 1), on one layer copy: each of the
-    seven outputs, honest and with every planted fault of `planted_faults`, checked by the bank
-    checker and by the row-sum checker of the in-pass path, at b = 128 and 256.  Per checker and
-    kind: outputs caught (some block rejected) of outputs, faulty blocks (y differs from the
-    honest output) caught, and false alarms (honest blocks rejected)."""
+    seven outputs, honest and with every planted fault of `campaign.planted_faults`, checked
+    by the bank checker and by the row-sum checker of the in-pass path, at b = 128 and 256,
+    K = 1 (the production setting; the K = 8 protocol is `campaign.py`'s).  Per checker and
+    kind: outputs caught (some block rejected) of outputs, faulty blocks caught, false alarms
+    (honest blocks rejected), and each escaped output's largest |rho| / tau.
+
+    The planted outputs are checked against the honest launch's row sums, so they test the
+    row-sum check on faults that arise after the products (reductions, partials, output).
+    Two further kinds plant the fault inside the producing in-pass launch, so that y and its
+    row sums come from the same faulty launch: a dropped tail of 4 columns (the launch run on
+    W with those columns zeroed) and a wrong activation vector (the launch run on another x).
+    These are reported apart, under ``inlaunch``: the bank check must catch them; the row-sum
+    check cannot, since d moves with y."""
     import torch
 
+    from campaign import planted_faults
     from pck.cuda import check_many, gemv_group_rowsums, rowsum_check_many
 
     gen = torch.Generator().manual_seed(seed)
     stats: dict = {}
+    inlaunch: dict = {}
     honest_blocks = 0
-    for name, _, _ in LAYER:
+
+    def count(c: dict, res, faulty=None) -> None:  # type: ignore[no-untyped-def]
+        v = res.verdict
+        c["outputs"] += 1
+        if faulty is None:  # honest output
+            c["false_alarms"] += int((~v).sum())
+            return
+        caught = bool((~v).any())
+        c["outputs_caught"] += int(caught)
+        c["faulty_blocks"] += int(faulty.sum())
+        c["faulty_blocks_caught"] += int((faulty & ~v).sum())
+        c["false_alarms"] += int((~faulty & ~v).sum())
+        if not caught:
+            c["escaped"].append(round(float((res.rho.abs() / res.tau).max()), 4))
+
+    def cell(d: dict, *keys: str) -> dict:  # type: ignore[type-arg]
+        for k in keys[:-1]:
+            d = d.setdefault(k, {})
+        return d.setdefault(keys[-1], {"outputs": 0, "outputs_caught": 0, "faulty_blocks": 0,
+                                       "faulty_blocks_caught": 0, "false_alarms": 0, "escaped": []})  # fmt: skip
+
+    for name, _, n in LAYER:
         ent = layer[name]
-        (y,), (sums,), _ = gemv_group_rowsums([(ent["W"], ent["x"])], (), THREADS)
-        cases = {"honest": y} | planted_faults(ent["W"], ent["x"], y, gen)
+        W, x = ent["W"], ent["x"]
+        (y,), (sums,), _ = gemv_group_rowsums([(W, x)], (), THREADS)
+        Wz = W.clone()
+        Wz.view(torch.uint8 if W.element_size() == 1 else torch.int16)[:, -4:] = 0
+        x2 = torch.randn(n, generator=gen).to(torch.bfloat16).to(x.device)
+        (yz, y2), (sz, s2), _ = gemv_group_rowsums([(Wz, x), (W, x2)], (), THREADS)
         for b in BLOCKS:
             bank, rows = ent["bank"][b], ent["rows"][b]
+            cases = {"honest": y} | planted_faults(W, x, y, gen, b)
             for kind, yy in cases.items():
+                faulty = None if kind == "honest" else (yy.view(-1, b) != y.view(-1, b)).any(dim=1)
+                if kind == "honest" and b == BLOCK:
+                    honest_blocks += y.numel() // b
+                count(cell(stats, f"b{b}", "bank", kind), check_many([(bank, x, yy)])[0], faulty)
+                count(cell(stats, f"b{b}", "rowsum", kind), rowsum_check_many([(rows, sums, yy)])[0], faulty)
+            for kind, yy, ss in (("drop_tail_4", yz, sz), ("wrong_x", y2, s2)):
                 faulty = (yy.view(-1, b) != y.view(-1, b)).any(dim=1)
-                for checker, res in (
-                    ("bank", check_many([(bank, ent["x"], yy)])[0]),
-                    ("rowsum", rowsum_check_many([(rows, sums, yy)])[0]),
-                ):
-                    v = res.verdict
-                    c = stats.setdefault(f"b{b}", {}).setdefault(checker, {}).setdefault(
-                        kind, {"outputs": 0, "outputs_caught": 0, "faulty_blocks": 0,
-                               "faulty_blocks_caught": 0, "false_alarms": 0})  # fmt: skip
-                    if kind == "honest":
-                        c["false_alarms"] += int((~v).sum())
-                        c["outputs"] += 1
-                        if b == BLOCK and checker == "bank":
-                            honest_blocks += v.numel()
-                        continue
-                    c["outputs"] += 1
-                    c["outputs_caught"] += int(bool((~v).any()))
-                    c["faulty_blocks"] += int(faulty.sum())
-                    c["faulty_blocks_caught"] += int((faulty & ~v).sum())
-                    c["false_alarms"] += int((~faulty & ~v).sum())
-    summary = {}
-    for bkey, per in stats.items():
-        for checker, kinds in per.items():
-            planted = {k: v for k, v in kinds.items() if k != "honest"}
-            summary[f"{checker}_{bkey}"] = {
-                "outputs_caught": f"{sum(v['outputs_caught'] for v in planted.values())}/"
-                                  f"{sum(v['outputs'] for v in planted.values())}",
-                "false_alarms": sum(v["false_alarms"] for v in kinds.values()),
-            }
-    return {"summary": summary, "by_kind": stats, "honest_blocks_b128": honest_blocks}
+                count(cell(inlaunch, f"b{b}", "bank", kind), check_many([(bank, x, yy)])[0], faulty)
+                count(cell(inlaunch, f"b{b}", "rowsum", kind), rowsum_check_many([(rows, ss, yy)])[0], faulty)
+
+    def summarize(per_block: dict, honest: bool) -> dict:  # type: ignore[type-arg]
+        out = {}
+        for bkey, per in per_block.items():
+            for checker, kinds in per.items():
+                planted = {k: v for k, v in kinds.items() if k != "honest"}
+                out[f"{checker}_{bkey}"] = {
+                    "outputs_caught": f"{sum(v['outputs_caught'] for v in planted.values())}/"
+                                      f"{sum(v['outputs'] for v in planted.values())}",
+                    "escapes": {k: v["escaped"] for k, v in planted.items() if v["escaped"]},
+                    "false_alarms": sum(v["false_alarms"] for v in kinds.values()),
+                } if honest else {k: f"{v['outputs_caught']}/{v['outputs']}" for k, v in planted.items()}
+        return out
+
+    return {"summary": summarize(stats, True), "inlaunch": summarize(inlaunch, False),
+            "by_kind": stats, "inlaunch_by_kind": inlaunch, "honest_blocks_b128": honest_blocks}
 
 
 def membership(copies: int = 4, reps: int = 20) -> dict:
@@ -746,6 +730,7 @@ def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: in
     import numpy as np
     import torch
 
+    from campaign import batched_faults
     from pck.cuda import GpuBlockedChecker, batched_height, check_batched, gemm_batched
     from pck.cuda import pack_batched_weights, quantize_fp8
 
@@ -858,38 +843,9 @@ def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: in
                 honest = ch.check_batched(X, Y).verdict
                 false_alarms += int((~honest).sum())
                 cells += honest.numel()
-                m, n = Y.size(1), X.size(1)
-                tally("bf16_output", ch.check_batched(X, Y.to(torch.bfloat16).float()))
-                for bit, kind in ((30, "exponent_flip"), (31, "sign_flip")):
-                    # top exponent bit of a random output / sign of the block's largest output
-                    y = Y.clone()
-                    blocks = m // BLOCK
-                    if bit == 31:
-                        sel = y.abs().view(B, blocks, BLOCK).argmax(dim=2)
-                    else:
-                        sel = torch.from_numpy(rng.integers(0, BLOCK, (B, blocks))).cuda()
-                    rows = sel + torch.arange(0, m, BLOCK, device=y.device)
-                    bits = y.view(torch.int32)
-                    bits.scatter_(1, rows, bits.gather(1, rows) ^ (1 << bit))
-                    tally(kind, ch.check_batched(X, y))
                 Wq = quantize_fp8(raw[0][idx])[0] if fp8 else raw[0][idx]
-                Wf = (Wq.float() if not fp8 else Wq.to(torch.float32)).t()  # (n, m)
-                Xf = X.float()
-                # dropped tail: the product skips the last 4 columns of every reduction
-                Wz = Wq.clone()
-                Wz.view(torch.uint8 if fp8 else torch.int16)[:, -4:] = 0
-                tally("skip_tail_4", ch.check_batched(X, gemm_batched(Wz, X)))
-                # BF16 partials: the 8 K segments' sums rounded to BF16 before they are added
-                seg = -(-n // 8)
-                yp = torch.zeros_like(Y)
-                for j in range(0, n, seg):
-                    yp += (Xf[:, j : j + seg] @ Wf[j : j + seg]).to(torch.bfloat16).float()
-                tally("bf16_partials", ch.check_batched(X, yp))
-                # BF16 accumulator: the running sum rounded to BF16 after every 32 columns
-                ya = torch.zeros_like(Y)
-                for j in range(0, n, 32):
-                    ya = (ya + Xf[:, j : j + 32] @ Wf[j : j + 32]).to(torch.bfloat16).float()
-                tally("bf16_accumulator", ch.check_batched(X, ya))
+                for kind, yy in batched_faults(Wq, X, Y, fp8, BLOCK, rng).items():
+                    tally(kind, ch.check_batched(X, yy))
             planted = sum(c[3] for c in kinds.values())
             caught = sum(c[2] for c in kinds.values())
             key = "fp8" if fp8 else "bf16"
@@ -1123,10 +1079,11 @@ def main() -> None:
         help="fewest rounds, no eager timing, no CPU baseline (for counter collection)",
     )  # fmt: skip
     parser.add_argument(
-        "--section", choices=("all", "b1", "templates", "members", "batched"), default="all",
+        "--section", choices=("all", "b1", "templates", "members", "batched", "campaign"),
+        default="all",
         help="b1: only the batch-1 layer (BF16 and FP8); templates: only the agent's templates; "
              "members: only the membership check and the vLLM plugin's step; batched: only the "
-             "batched layer (B = 128, 256)",
+             "batched layer (B = 128, 256); campaign: only the detection campaign (K = 8)",
     )  # fmt: skip
     args = parser.parse_args()
     if args.quick:
@@ -1138,6 +1095,8 @@ def main() -> None:
 
     import torch
 
+    import campaign
+    from campaign import contract_summary
     from pck.cuda.timing import read_bandwidth_gbps, read_stream_ms
 
     if args.section == "templates":
@@ -1148,6 +1107,9 @@ def main() -> None:
         return
     if args.section == "batched":
         print(json.dumps({"batched": batched_layer(reps=3 if args.quick else 7)}), flush=True)
+        return
+    if args.section == "campaign":
+        print(json.dumps({"detection_k8": contract_summary(campaign.run(quick=args.quick))}), flush=True)
         return
     depth = 32  # a Llama-3-8B decode pass
     # At least 7 alternating rounds whatever --steps is; each round replays one 32-layer pass
@@ -1176,8 +1138,11 @@ def main() -> None:
             for kind, w in (("bf16", 2), ("fp8", 1))
         },
     }
-    member = plugin = sampling = batched = templates = None
+    member = plugin = sampling = batched = templates = detection = None
     if args.section == "all":
+        print("[bench] running the detection campaign (K = 8)", file=sys.stderr, flush=True)
+        detection = campaign.run(quick=args.quick)
+        detail["detection_k8"] = detection
         print("[bench] timing the membership check", file=sys.stderr, flush=True)
         member = membership()
         print("[bench] timing the vLLM plugin's wrapper per step", file=sys.stderr, flush=True)
@@ -1241,8 +1206,11 @@ def main() -> None:
         },
         "checker_overhead_pct": ovh(b16),
         "fp8_checker_overhead_pct": ovh(b8),
-        "faults_b1": {"bf16": b16["faults"]["summary"], "fp8": b8["faults"]["summary"]},
+        "faults_b1": {"bf16": b16["faults"]["summary"], "fp8": b8["faults"]["summary"],
+                      "inlaunch": {"bf16": b16["faults"]["inlaunch"], "fp8": b8["faults"]["inlaunch"]}},
     }
+    if detection is not None:
+        line["detection_k8"] = contract_summary(detection)
     if member is not None:
         line["membership"] = {k: member[k] for k in ("ms", "gbps", "pct_of_peak", "planted_caught", "false_alarms")}
     if plugin is not None:

@@ -281,13 +281,20 @@ int pck_batch_check(const PckBatchCheckDesc* descs, int count, void* workspace,
  * the reference: it is for callers that cannot allocate device memory (code under HIP graph
  * capture, serving loops that forbid hipMalloc).  The partial sums go to a file-scope device
  * array of pck_batch_check_static_bytes() bytes (16 MiB), one per GPU the library runs on,
- * held until the process ends; its address is looked up once per device, on the first call
- * with that device current.  A plan that needs more than that returns hipErrorOutOfMemory
+ * held until the process ends.  Its address on a device is looked up once, by
+ * pck_batch_check_static_init() called with that device current, or else by the first
+ * pck_batch_check_static call with that device current.  The lookup is a HIP runtime call
+ * (hipGetSymbolAddress), so a caller whose first call on a device may be under HIP graph
+ * capture calls pck_batch_check_static_init() on that device beforehand, outside the capture;
+ * after that no call makes a runtime call other than its two kernel launches.  init returns a
+ * hipError_t and may be called again (it then does nothing).  A plan that needs more than that
+ * returns hipErrorOutOfMemory
  * (a Llama-3-8B decode layer needs 6.5 MiB at batch 128 or 256); invalid descriptors return
  * hipErrorInvalidValue as for pck_batch_check; in both cases nothing is enqueued.  Every
  * call on one GPU shares its array: calls that overlap on one GPU (different streams, or
  * different host threads) race.  Nothing in the array needs clearing between calls. */
 int64_t pck_batch_check_static_bytes(void);
+int pck_batch_check_static_init(void);
 int pck_batch_check_static(const PckBatchCheckDesc* descs, int count, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
@@ -309,9 +316,11 @@ int pck_check_members(const float* logits, int64_t rows, int64_t vocab, const in
 /* The same check with the options a sampler hook needs in one launch (the reference's plugin
  * builds these with torch ops around its check, src/pck/vllm_plugin.py:146-186):
  *   top_p            FP64, or FP32 when top_p_fp32 = 1 (widened exactly), or NULL;
- *   temperature      (requests,) FP32 with temperature_index (rows,) int64: row r is greedy
- *                    iff temperature[temperature_index[r]] == 0 (vLLM's per-request sampling
- *                    state); NULL: greedy as in pck_check_members;
+ *   temperature      (temperature_count,) FP32 with temperature_index (rows,) int64: row r is
+ *                    greedy iff temperature[temperature_index[r]] == 0 (vLLM's per-request
+ *                    sampling state); a row whose index lies outside [0, temperature_count)
+ *                    is rejected (ok = 0, counted as rejected) and the array is not read for
+ *                    it; NULL: greedy as in pck_check_members (temperature_count unused);
  *   injected         (rows,) uint8 faults the caller planted, or NULL;
  *   ok, above, mass_above   outputs as in pck_check_members; each may be NULL;
  *   totals           NULL, or 6 words the kernel adds each row into (64-bit atomics):
@@ -333,6 +342,7 @@ typedef struct PckMemberArgs {
   const uint8_t* greedy;
   const float* temperature;
   const int64_t* temperature_index;
+  int64_t temperature_count;
   const uint8_t* injected;
   double slack;
   int64_t k_lim;

@@ -693,6 +693,11 @@ extern "C" int pck_batch_check(const PckBatchCheckDesc* descs, int count, void* 
 
 extern "C" int64_t pck_batch_check_static_bytes(void) { return pck::kScratchBytes; }
 
+extern "C" int pck_batch_check_static_init(void) {
+  hipError_t err = hipSuccess;
+  return pck::scratch_address(err) != nullptr ? hipSuccess : err;
+}
+
 extern "C" int pck_batch_check_static(const PckBatchCheckDesc* descs, int count, void* stream) {
   pck::Plan plan{};
   const int64_t need = pck::make_plan(descs, count, plan);

@@ -308,8 +308,11 @@ __global__ void __launch_bounds__(kThreads) member_kernel(const MemberArgs A) {
   const int64_t k_req = A.top_k ? A.top_k[r] : vocab;
   const int64_t k_row = k_req < 1 ? 1 : (k_req > vocab ? vocab : k_req);
   // Greedy rows: the caller's flags, or temperature 0 of the row's request (vLLM's sampling
-  // state, read through the row's request index).
-  const bool greedy = A.temperature ? A.temperature[A.temperature_index[r]] == 0.0f
+  // state, read through the row's request index).  A request index outside the temperature
+  // array rejects the row without reading it.
+  const int64_t request = A.temperature ? A.temperature_index[r] : 0;
+  const bool request_ok = !A.temperature || (request >= 0 && request < A.temperature_count);
+  const bool greedy = A.temperature ? request_ok && A.temperature[request_ok ? request : 0] == 0.0f
                                     : (A.greedy ? A.greedy[r] != 0 : false);
   const bool has_p = A.top_p != nullptr;
   const double p = !has_p ? 1.0
@@ -405,7 +408,7 @@ __global__ void __launch_bounds__(kThreads) member_kernel(const MemberArgs A) {
   float m = lane_max;
   group_reduce(above, any_nan, m, s);
 
-  bool ok = !any_nan && in_range && above < (greedy ? 1 : k_row);
+  bool ok = request_ok && !any_nan && in_range && above < (greedy ? 1 : k_row);
   double mass = 0.0;
   if (want_mass) {
     double z = 0.0;
@@ -476,7 +479,8 @@ extern "C" int pck_check_members_ex(const PckMemberArgs* args, void* stream) {
       a.vocab > 0x7FFFFFFF || a.k_lim < 0 || a.k_lim > a.vocab)
     return hipErrorInvalidValue;
   if (a.rows == 0) return hipSuccess;
-  if (!a.logits || !a.tokens || (a.temperature && !a.temperature_index)) return hipErrorInvalidValue;
+  if (!a.logits || !a.tokens || (a.temperature && (!a.temperature_index || a.temperature_count < 1)))
+    return hipErrorInvalidValue;
   if (a.all_k && a.k_lim < 1) return hipErrorInvalidValue;
   pck::member_kernel<<<dim3(static_cast<unsigned>(a.rows)), dim3(pck::kThreads), 0,
                        static_cast<hipStream_t>(stream)>>>(a);

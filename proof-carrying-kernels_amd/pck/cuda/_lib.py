@@ -123,6 +123,7 @@ class PckMemberArgs(ctypes.Structure):
         ("greedy", _p),
         ("temperature", _p),
         ("temperature_index", _p),
+        ("temperature_count", _i64),
         ("injected", _p),
         ("slack", _f64),
         ("k_lim", _i64),
@@ -156,6 +157,7 @@ SIGNATURES: dict[str, list[Any]] = {
     "pck_batch_check_workspace": [ctypes.POINTER(PckBatchCheckDesc), _int, ctypes.POINTER(_i64)],
     "pck_batch_check": [ctypes.POINTER(PckBatchCheckDesc), _int, _p, _i64, _p],
     "pck_batch_check_static": [ctypes.POINTER(PckBatchCheckDesc), _int, _p],
+    "pck_batch_check_static_init": [],
     "pck_read_stream": [_p, _i64, _p, _int, _p],
     "pck_check_members": [
         _p, _i64, _i64, _p, _p, _p, _p, _f64, _i64, _int, _p, _p, _p, _p,

@@ -148,7 +148,7 @@ def launch_check(
 
     Beside `check_members`'s arguments: ``temperature`` (requests,) FP32 with
     ``temperature_index`` (B,) makes row r greedy iff temperature[index[r]] == 0 (instead of
-    ``greedy``); ``top_p`` may be FP32 (read as is) or FP64; ``injected`` (B,) bool marks planted
+    ``greedy``), and rejects a row whose index is outside [0, requests); ``top_p`` may be FP32 (read as is) or FP64; ``injected`` (B,) bool marks planted
     faults; ``totals`` (from `new_totals`) receives the batch's counts on the device.  Returns
     the outputs (``ok``, ``above``, ``mass_above``) unless ``outputs`` is False.  Never
     synchronises: top-k's host copy is ``top_k_host`` (or one copy of ``top_k``)."""
@@ -191,6 +191,7 @@ def launch_check(
         t = temperature.to(device=device, dtype=torch.float32).contiguous()
         keep.append(t)
         a.temperature = t.data_ptr()
+        a.temperature_count = t.numel()
         a.temperature_index = dev(temperature_index, torch.long, "temperature_index")
     elif greedy is not None:  # a bool tensor is read as its bytes (0 or 1)
         g = greedy.to(device=device, dtype=torch.bool).reshape(rows).contiguous().view(torch.uint8)

@@ -193,3 +193,25 @@ def test_top_k_outside_one_to_vocab_is_clamped_like_the_reference() -> None:
     # candidates meet in LDS in arrival order, so the FP64 sums may differ in their last bits
     assert np.all(np.abs(got["mass_above"] - want["mass_above"]) <= 2 * member_eps32(300))
     assert_matches_oracle(logits, tokens, clamped, np.full(6, 0.9), top_k_host=clamped)
+
+
+def test_request_index_outside_the_temperature_array_rejects_the_row() -> None:
+    """The sampler-hook entry reads greedy through a per-row request index: an index outside
+    [0, len(temperature)) rejects that row (counted as rejected in the device totals) without
+    reading past the array, and the other rows keep their verdicts."""
+    from pck.member import launch_check, new_totals
+
+    rng = np.random.default_rng(11)
+    rows, vocab = 8, 3000
+    logits = torch.from_numpy(rng.standard_normal((rows, vocab)).astype(np.float32)).cuda()
+    tokens = logits.argmax(dim=1)  # allowed under any top-k / top-p: every row passes
+    temperature = torch.tensor([0.0, 1.0, 0.7], device="cuda")
+    good = torch.tensor([0, 1, 2, 1, 0, 2, 1, 0], device="cuda")
+    ref = launch_check(logits, tokens, temperature=temperature, temperature_index=good)
+    assert bool(ref["ok"].all())
+    bad = good.clone()
+    bad[2], bad[5] = 3, -1  # past the end, negative
+    totals = new_totals(logits.device)
+    out = launch_check(logits, tokens, temperature=temperature, temperature_index=bad, totals=totals)
+    assert out["ok"].tolist() == [True, True, False, True, True, False, True, True]
+    assert int(totals[0]) == rows and int(totals[1]) == 2

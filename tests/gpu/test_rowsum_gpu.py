@@ -188,9 +188,48 @@ def test_verdicts_equal_bank_checker(fp8: bool, m: int, n: int) -> None:
         in_window += int((~clear).sum())
         if name == "honest":
             assert va.all() and vb.all()
-        elif name in ("exp_flip", "sign_flip", "drop_tail", "bf16_accumulator"):
-            assert not vb.all(), f"{name} not caught"
     print(f"blocks between the two thresholds: {in_window}", flush=True)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("m,n", [(4096, 4096), (4096, 14336)])
+def test_every_planted_fault_caught_at_eight_draws(fp8: bool, m: int, n: int) -> None:
+    """The reference's protocol for planted shortcuts (8 sign draws, harness/numerics_sim.py:76):
+    with y faulty after the products (the campaign's faults against the honest launch's row
+    sums), both the row-sum and the bank check catch every kind at b = 128."""
+    print(f"planted faults at K = 8 fp8={fp8} m={m} n={n}", flush=True)
+    W, x, Wv, xv = weights(m, n, seed=m + n + 1, fp8=fp8)
+    ys, sums, _ = gemv_group_rowsums([(W, x)], (), 256)
+    h = tree_height(n, 256, 16 if fp8 else 8)
+    bank = GpuBlockedChecker(W.to(torch.bfloat16), 128, h, checks=8, generator=torch.Generator().manual_seed(7))
+    rs = RowSumChecker(m, n, 128, h, checks=8, generator=torch.Generator().manual_seed(7))
+    y = ys[0].cpu().numpy()
+    for name, yy in planted(Wv, xv, y, seed=n + 1).items():
+        yt = torch.from_numpy(np.ascontiguousarray(yy, dtype=np.float32)).cuda()
+        assert not bool(check_many([(bank, x, yt)])[0].verdict.all()), f"bank: {name} not caught"
+        assert not bool(rs.check(sums[0], yt).verdict.all()), f"row sums: {name} not caught"
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_faults_inside_the_producing_launch(fp8: bool) -> None:
+    """The row-sum check's trust model.  A shortcut inside the producing launch moves y and its
+    row sums together: the in-pass launch run on W with its last 4 columns zeroed (a dropped
+    tail) or on another x (a wrong activation vector) writes y and (d, s) that agree with each
+    other, so the row-sum check passes them, as it passes honest outputs; the bank checker,
+    whose checksums come from the weights and x themselves, rejects them.  Faults after the
+    products (reductions, partials, output, flips) are the row-sum check's domain."""
+    m, n = 4096, 4096
+    W, x, _, _ = weights(m, n, seed=21, fp8=fp8)
+    h = tree_height(n, 256, 16 if fp8 else 8)
+    bank = GpuBlockedChecker(W.to(torch.bfloat16), 128, h, generator=torch.Generator().manual_seed(9))
+    rs = RowSumChecker(m, n, 128, h, generator=torch.Generator().manual_seed(9))
+    Wz = W.clone()
+    Wz.view(torch.uint8 if fp8 else torch.int16)[:, -4:] = 0
+    x2 = torch.randn(n, generator=torch.Generator().manual_seed(22)).to(torch.bfloat16).cuda()
+    (yz, y2), (sz, s2), _ = gemv_group_rowsums([(Wz, x), (W, x2)], (), 256)
+    for name, yy, ss in (("drop_tail", yz, sz), ("wrong_x", y2, s2)):
+        assert bool(rs.check(ss, yy).verdict.all()), f"row sums from the faulty launch: {name}"
+        assert not bool(check_many([(bank, x, yy)])[0].verdict.all()), f"bank: {name} not caught"
 
 
 def test_non_finite_fails_closed() -> None:

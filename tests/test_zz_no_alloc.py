@@ -4,7 +4,9 @@
   (check, block, column)) on two calls in a row: a Llama-3-8B decode layer at batch 128 with
   planted faults, then a smaller layer at batch 33 (the second call reuses the device array
   the first one left its partial sums in);
-- replays of a HIP graph that captured it equal the eager call, with eager work between;
+- replays of a HIP graph that captured it equal the eager call, with eager work between,
+  also in a fresh process whose first call is the captured one (after
+  pck_batch_check_static_init, the lookup of the array's address, outside the capture);
 - on the host, with no GPU: a plan beyond the static array returns hipErrorOutOfMemory and an
   invalid descriptor hipErrorInvalidValue, both before any HIP call (the descriptors' pointers
   are never dereferenced there).
@@ -102,11 +104,8 @@ def test_graph_replays_equal_the_eager_call() -> None:
     items = layer(LLAMA[:2], 64, 3, faults=True)
     want = with_workspace(items)
     descs, results, device = batched_descriptors(items)
-    side = torch.cuda.Stream(device)
-    side.wait_stream(torch.cuda.current_stream(device))
-    with torch.cuda.stream(side):  # warm the per-device address lookup outside the capture
-        check(lib().pck_batch_check_static(descs, len(items), stream_handle(device)), "warm-up")
-    torch.cuda.current_stream(device).wait_stream(side)
+    with torch.cuda.device(device):  # the per-device address lookup, outside the capture
+        check(lib().pck_batch_check_static_init(), "pck_batch_check_static_init")
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
@@ -124,6 +123,47 @@ def test_graph_replays_equal_the_eager_call() -> None:
         assert_bitwise_equal(results, want)
         with_workspace(items)  # eager use of the same checker between replays
         torch.cuda.synchronize()
+
+
+FIRST_CALL_UNDER_CAPTURE = """
+import sys, torch
+sys.path[:0] = [{root!r}, {root!r} + "/proof-carrying-kernels_amd"]
+from tests.test_zz_no_alloc import LLAMA, assert_bitwise_equal, layer, with_workspace
+from pck.cuda._lib import check, lib, stream_handle
+from pck.cuda.checker import batched_descriptors
+items = layer(LLAMA[2:4], 40, 5, faults=True)
+want = with_workspace(items)
+descs, results, device = batched_descriptors(items)
+check(lib().pck_batch_check_static_init(), "init")
+torch.cuda.synchronize()
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):
+    err = lib().pck_batch_check_static(descs, len(items), stream_handle(device))
+check(err, "first pck_batch_check_static call, under capture")
+for replay in range(2):
+    graph.replay()
+    torch.cuda.synchronize()
+    assert_bitwise_equal(results, want)
+print("first call under capture: replays equal the workspace entry")
+"""
+
+
+@pytest.mark.gpu
+@gpu
+def test_first_call_of_a_fresh_process_under_capture() -> None:
+    """In a fresh process (no earlier call has looked the array up), pck_batch_check_static_init
+    and then a first call made under graph capture: every replay equals pck_batch_check."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = str(Path(__file__).resolve().parent.parent)
+    print("fresh process: first static call under capture", flush=True)
+    done = subprocess.run([sys.executable, "-c", FIRST_CALL_UNDER_CAPTURE.format(root=root)],
+                          capture_output=True, text=True, timeout=110, cwd=root)  # fmt: skip
+    print(done.stdout[-2000:], done.stderr[-2000:], flush=True)
+    assert done.returncode == 0
+    assert "replays equal the workspace entry" in done.stdout
 
 
 def fake_desc(m: int, n: int, B: int, checks: int) -> PckBatchCheckDesc:
