@@ -8,7 +8,7 @@
 //   r[k, beta, :] in {-1, +1}                   int8, secret
 // For every check k and row block beta (reference src/pck/cuda/csrc/checker_kernel.cu:49-91):
 //   rho = c . x - r . y_beta
-//   s   = a . |x|                               every operation rounded up, then up to FP32
+//   s   = a . |x|                               every operation rounded up
 //   tau = coef s + geps ((1 + u32) s + sum |y_beta|) + tau_floor, every operation rounded up
 // and the block passes only if every y in it is finite, tau is finite and |rho| <= tau.
 //
@@ -17,9 +17,13 @@
 // FP64 operation, so rho's rounding error is at most gamma_H(u64) (sum |c_j x_j| + sum |y_i|)
 // for the depth H <= n + b + 1 of its evaluation, which the host's geps (reference formula,
 // which also carries the reference's FP32 Dot2 term) covers.  s and the sums of |y| add exact
-// non-negative terms with error-free round-up additions; s is then rounded up to FP32 once, so
-// an a . |x| beyond the FP32 range gives s = inf, tau = inf and a failed block, the reference's
-// fail-closed overflow.  tau's products and sums use the general round-up operations.
+// non-negative terms (a_j |x_j| has 16 significand bits) with error-free round-up additions in
+// FP64.  The reference adds the same terms in FP32, rounding up, and then in FP64; since every
+// FP32 partial it forms is at least the exact sum, and the FP64 sums here are exact whenever
+// its FP32 ones are, this s is at most the reference's (equal on typical inputs), and so is
+// tau.  An s beyond the FP32 range becomes +inf (tau = inf, a failed block), as the
+// reference's FP32 sum would overflow.  tau's products and sums use the general round-up
+// operations.
 //
 // Order.  Lane t accumulates the y terms of rows t, t + 256, ..., then the bank quads t,
 // t + 256, t + 512, ... in increasing order (four accumulators per quantity, one per column of a
@@ -57,11 +61,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                            static_cast<int>(bytes), 0x00020000);
 }
 
-// The smallest FP32 value >= v (v >= 0), widened back to FP64; +inf beyond the FP32 range.
+// The smallest FP32 value >= v (v >= 0), widened back to FP64; +inf beyond the FP32 range
+// (the batched checker's bound on s).
 __device__ __forceinline__ double round_up_to_f32(double v) {
   float f = static_cast<float>(v);
   if (static_cast<double>(f) < v) f = __uint_as_float(__float_as_uint(f) + 1u);  // v >= 0
   return static_cast<double>(f);
+}
+
+// v (>= 0) if it lies within the FP32 range, else +inf: the threshold fails closed where the
+// reference's FP32 sum of |a x| would overflow.
+__device__ __forceinline__ double within_f32_range(double v) {
+  return v <= static_cast<double>(__FLT_MAX__) ? v : __builtin_inf();
 }
 
 // The four per-lane quantities: c.x and r.y round to nearest, s and sum |y| round up.
@@ -183,7 +194,7 @@ __device__ __forceinline__ void check_pair(const PckCheckBatch& batch, int64_t i
 
   const Quad total = group_sum(q, lds);
   if (t == 0) {
-    const double s_up = round_up_to_f32(total.s);
+    const double s_up = within_f32_range(total.s);
     const double rho = total.cx - total.ry;
     const double cabs_up = mul_up(kOnePlusU32, s_up);
     const double eps = mul_up(d.geps, add_up(cabs_up, total.yabs));

@@ -380,3 +380,46 @@ def test_many_layers_overlap_and_detect_a_fault() -> None:
             assert not v[0] and v[1:].all()
         else:
             assert v.all()
+
+
+# (m, n, block, checks): quad loads (n % 4 == 0) and element loads (n % 4 != 0), block sizes
+# below, at and above the 256 lanes that take the y rows, the Llama-3-8B widths.
+BIT_CASES = [(512, 4096, 128, 2), (256, 14336, 128, 1), (512, 4100, 64, 3), (512, 1001, 512, 2),
+             (64, 4096, 8, 4), (256, 4096, 256, 1)]  # fmt: skip
+
+
+@pytest.mark.parametrize(("m", "n", "block", "checks"), BIT_CASES)
+def test_passed_rho_tau_equal_the_hip_model_bit_for_bit(m: int, n: int, block: int, checks: int) -> None:
+    """The kernel's (passed, rho, tau) equal `oracle.checker_orders.hip_check` bit for bit, on
+    an honest output, one with a BF16-rounded tail and flipped exponent and sign bits, and one
+    with a NaN and an infinity; and its tau is never above the reference CUDA kernel's
+    (`reference_gpu_check`) at the segment count the reference would choose on its 30-SM GPU."""
+    from oracle.checker_orders import hip_check, reference_default_segments, reference_gpu_check
+
+    print(f"checker bits m={m} n={n} b={block} K={checks}", flush=True)
+    _, x, Wt, xt = problem(m, n, seed=m + n)
+    h = tree_height(n, THREADS, 8)
+    ch = GpuBlockedChecker(Wt, block, h, checks=checks, generator=torch.Generator().manual_seed(n))
+    y = gemv_coalesced(Wt, xt, THREADS)
+    bad = y.clone()
+    bad[m // 2 :] = bad[m // 2 :].bfloat16().float()
+    bits = bad.view(torch.int32)
+    bits[1] ^= 1 << 27
+    bits[m - 2] ^= -(2**31)
+    odd = y.clone()
+    odd[block // 2] = float("nan")
+    odd[m - 1] = float("inf")
+    c, a, r = ch.c.cpu().numpy(), ch.a.float().cpu().numpy(), ch.r.cpu().numpy()
+    seg = reference_default_segments(n, checks, ch.num_blocks, 30)
+    for name, yy in (("honest", y), ("faulty", bad), ("non-finite", odd)):
+        res = check_many([(ch, xt, yy)])[0]
+        yn = yy.cpu().numpy()
+        passed, rho, tau = hip_check(c, a, r, x, yn, ch.coef, ch.geps, ch.tau_floor)
+        assert np.array_equal(res.passed.cpu().numpy(), passed), name
+        for got, want in ((res.rho.cpu().numpy(), rho), (res.tau.cpu().numpy(), tau)):
+            same = (got.view(np.uint64) == want.view(np.uint64)) | (np.isnan(got) & np.isnan(want))
+            assert same.all(), (name, np.argwhere(~same)[:4])
+        _, _, tau_ref = reference_gpu_check(c, a, r, x, yn, ch.coef, ch.geps, ch.tau_floor, seg)
+        finite = np.isfinite(tau_ref)
+        assert (res.tau.cpu().numpy()[finite] <= tau_ref[finite]).all(), name
+    assert bool(check_many([(ch, xt, y)])[0].passed.all())
