@@ -24,12 +24,13 @@
 //   the prefix are >= L0 and L0 is a lower bound of the row's kth (the k-th largest of a part
 //   never exceeds that of the whole).
 //   Stream (the rest of the row, read from HBM once, non-temporal): count above, NaN flag, row
-//   maximum, and the logits >= L0 compacted into LDS (ballot + one LDS atomic per wave); then
-//   the prefix, held in registers (or re-read from L2 for unaligned or short rows), is
-//   compacted too.  For LLM logits that is a few hundred values; kth
-//   and both sums come from LDS with no further pass over the row.  If more than kCap values
-//   qualify (flat or adversarial rows), an exact 4-pass radix select over the row and a summing
-//   pass take over.  Rows without a top-k sum over the whole row in a second pass.
+//   maximum, and the logits >= L0 compacted into LDS, each wave into its own segment of kSeg
+//   slots (a ballot per step; the wave's count is uniform, so no atomics); then the prefix,
+//   held in registers (or re-read from L2 for unaligned or short rows), is compacted too.  For
+//   LLM logits that is a few hundred values (a few dozen per wave); kth and both sums come from
+//   LDS with no further pass over the row, each wave reading back its own segment.  If more
+//   than kSeg values qualify in one wave (flat or adversarial rows), an exact 4-pass radix
+//   select over the row and a summing pass take over.  Rows without a top-k sum over the whole row in a second pass.
 
 #include <hip/hip_runtime.h>
 
@@ -45,6 +46,7 @@ constexpr int kThreads = 1024;
 constexpr int kWave = 64;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kCap = 4096;  // candidates held in LDS
+constexpr int kSeg = kCap / kWaves;  // candidates each wave holds, in its own segment
 constexpr int64_t kPrefix = 16 * kThreads;  // logits that set the candidate threshold
 
 using MemberArgs = PckMemberArgs;
@@ -81,13 +83,11 @@ __device__ __forceinline__ float split_term(float x, float m) {
 
 struct Scratch {
   float cand[kCap];
-  uint32_t lane_key[kThreads];
   uint32_t hist[2][256];
   double red_d[2][kWaves];
   int64_t red_i[kWaves];
   float red_f[kWaves];
   int red_flag[kWaves];
-  int count;
   uint32_t digit[2];
   int64_t rank[2];
 };
@@ -221,12 +221,13 @@ __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
   return static_cast<uint32_t>(a);
 }
 
-// Key of the rank-th largest (1-based) of `count` keys given by key_of(i), by an exact radix
-// select over 8-bit digits with an LDS histogram.  Every lane returns the same key.  With
+// Key of the rank-th largest (1-based) of the workgroup's keys, by an exact radix select over
+// 8-bit digits with an LDS histogram.  visit(f) calls f(key) for each key a lane holds, in
+// the same way on every round (each key by one lane).  Every lane returns the same key.  With
 // kRounds < 4 only the top 8 kRounds bits are selected and the rest are zero: the result is
 // the smallest key of the bucket that holds the rank-th largest.
-template <int kRounds = 4, typename K>
-__device__ uint32_t radix_select(int64_t count, int64_t rank, K&& key_of, Scratch& s) {
+template <int kRounds = 4, typename V>
+__device__ uint32_t radix_select(int64_t rank, V&& visit, Scratch& s) {
   const int t = static_cast<int>(threadIdx.x);
   uint32_t prefix = 0;
   uint32_t mask = 0;
@@ -243,8 +244,7 @@ __device__ uint32_t radix_select(int64_t count, int64_t rank, K&& key_of, Scratc
     const int shift = 24 - 8 * round;
     const int cur = round & 1;
     if (round > 0 && t < 256) s.hist[cur ^ 1][t] = 0;
-    for (int64_t i = t; i < count; i += kThreads) {
-      const uint32_t k = key_of(i);
+    visit([&](uint32_t k) {
       const bool hit = (k & mask) == prefix;
       const uint32_t digit = (k >> shift) & 255u;
       // Keys bunch into a few buckets (one exponent byte for every candidate): a wave whose
@@ -257,7 +257,7 @@ __device__ uint32_t radix_select(int64_t count, int64_t rank, K&& key_of, Scratc
       } else if (hit) {
         atomicAdd(&s.hist[cur][digit], 1u);
       }
-    }
+    });
     __syncthreads();
     if (wave_id() == 0) {
       // lane l owns digits 255 - 4l ... 252 - 4l (descending); scan lanes in order
@@ -353,27 +353,28 @@ __global__ void __launch_bounds__(kThreads) member_kernel(const MemberArgs A) {
   // It is selected while the stream's first loads are in flight.
   float low = -__builtin_inff();
   auto threshold = [&] {
-    s.lane_key[t] = order_key(lane_max);
-    if (t == 0) s.count = 0;
-    __syncthreads();
-    low = key_value(radix_select<2>(kThreads, k_eff, [&](int64_t i) { return s.lane_key[i]; }, s));
+    const uint32_t key = order_key(lane_max);
+    low = key_value(radix_select<2>(k_eff, [&](auto&& f) { f(key); }, s));
     if (low != low) low = -__builtin_inff();
   };
-  // Compacts every logit >= low into LDS (lanes may diverge at the end of a range).
+  // Compacts every logit >= low into the wave's LDS segment.  The wave's count follows the
+  // ballots, so no atomic is needed.  Lanes may diverge at the end of a range: the lanes that
+  // run a step are then always a prefix of the wave from its lane 0 (a lane's trip count never
+  // exceeds that of a lower lane), so lane 0 runs every step and holds the wave's count, and
+  // each step takes the count from the first active lane.
+  float* const seg = s.cand + wave_id() * kSeg;
+  int wcount = 0;
   auto compact = [&](float l) {
     const bool take = l >= low;
     const uint64_t want = __ballot(take);
     if (want != 0) {
-      const uint64_t active = __ballot(1);
-      const int leader = __builtin_ctzll(active);
-      int base = 0;
-      if (lane_id() == leader) base = atomicAdd(&s.count, __builtin_popcountll(want));
-      base = __shfl(base, leader, kWave);
+      const int base = __builtin_amdgcn_readfirstlane(wcount);
       if (take) {
         const uint64_t below = lane_id() ? want & (~0ull >> (kWave - lane_id())) : 0ull;
         const int at = base + __builtin_popcountll(below);
-        if (at < kCap) s.cand[at] = l;
+        if (at < kSeg) seg[at] = l;
       }
+      wcount = base + __builtin_popcountll(want);
     }
   };
   // Most quads hold no candidate: one ballot per quad decides whether any lane needs compact.
@@ -403,10 +404,15 @@ __global__ void __launch_bounds__(kThreads) member_kernel(const MemberArgs A) {
   } else {
     for_each<true>(row, prefix, vocab, scan);
   }
+  // bit 0: a NaN in the row; bit 1: a wave's segment overflowed (every lane runs here, so the
+  // first active lane is lane 0)
+  wcount = __builtin_amdgcn_readfirstlane(wcount);
   int64_t above = above_lane;
-  int any_nan = nan;
+  int flags = nan | (wcount > kSeg ? 2 : 0);
   float m = lane_max;
-  group_reduce(above, any_nan, m, s);
+  group_reduce(above, flags, m, s);
+  const bool any_nan = flags & 1;
+  const bool overflow = flags & 2;
 
   bool ok = request_ok && !any_nan && in_range && above < (greedy ? 1 : k_row);
   double mass = 0.0;
@@ -419,12 +425,13 @@ __global__ void __launch_bounds__(kThreads) member_kernel(const MemberArgs A) {
         z += e;
         a += l > lt ? e : 0.0;
       });
-    } else if (fused && s.count <= kCap) {
-      const int64_t count = s.count;
-      const float kth = key_value(
-          radix_select(count, k_eff, [&](int64_t i) { return order_key(s.cand[i]); }, s));
-      for (int64_t i = t; i < count; i += kThreads) {
-        const float l = s.cand[i];
+    } else if (fused && !overflow) {
+      // each wave reads back its own segment (LDS is in order within a wave)
+      const float kth = key_value(radix_select(k_eff, [&](auto&& f) {
+        for (int j = lane_id(); j < wcount; j += kWave) f(order_key(seg[j]));
+      }, s));
+      for (int j = lane_id(); j < wcount; j += kWave) {
+        const float l = seg[j];
         if (l >= kth) {
           const float e = split_term(l, m);
           z += e;
@@ -432,8 +439,9 @@ __global__ void __launch_bounds__(kThreads) member_kernel(const MemberArgs A) {
         }
       }
     } else {
-      const float kth = key_value(
-          radix_select(vocab, k_eff, [&](int64_t i) { return order_key(row[i]); }, s));
+      const float kth = key_value(radix_select(k_eff, [&](auto&& f) {
+        for (int64_t i = t; i < vocab; i += kThreads) f(order_key(row[i]));
+      }, s));
       for_each<false>(row, 0, vocab, [&](float l) {
         if (l >= kth) {
           const float e = split_term(l, m);

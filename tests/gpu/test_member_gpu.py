@@ -108,14 +108,31 @@ def test_nan_rows_reject() -> None:
     assert not out["ok"][1] and out["ok"][0] == check_member(logits[0], 0, top_p=0.999999).ok
 
 
-@pytest.mark.parametrize("case", ["all_equal", "many_ties", "k_above_1024", "keep_all_rows", "mixed"])
+CASES = ["all_equal", "many_ties", "k_above_1024", "keep_all_rows", "mixed", "k_700",
+         "one_wave_overflows"]  # fmt: skip
+
+
+@pytest.mark.parametrize("case", CASES)
 def test_fallback_paths_match_the_oracle(case: str) -> None:
-    """Rows whose candidate set overflows LDS, k_eff above 1024, rows without top-k."""
+    """Rows whose candidate set overflows LDS, k_eff above 1024, rows without top-k; k_700
+    leaves ~1400 candidates (several per lane of each wave's segment, none overflowing) and
+    one_wave_overflows puts 512 equal maxima in the stream slots of one wave only (that wave's
+    segment overflows while the row's total fits)."""
     rng = np.random.default_rng(5)
     rows, vocab = 8, 20000
+    if case == "one_wave_overflows":
+        rows, vocab = 2, 151_936
     logits = (rng.standard_normal((rows, vocab)) * 2).astype(np.float32)
     top_k = np.full(rows, 50)
-    if case == "all_equal":
+    if case == "k_700":
+        top_k[:] = 700
+    elif case == "one_wave_overflows":
+        # the stream starts at logit 16384; lane t of the workgroup reads quad 4096 + t +
+        # 1024 j, so wave 3 (lanes 192..255) reads logits 16384 + 4096 j + 768 .. + 1023
+        for j in range(2):
+            start = 16384 + 4096 * j + 768
+            logits[:, start : start + 256] = 50.0
+    elif case == "all_equal":
         logits[:] = 1.25
     elif case == "many_ties":
         logits[:, : vocab // 2] = 3.0  # 10000 values tied at the top
