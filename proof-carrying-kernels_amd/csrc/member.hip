@@ -82,31 +82,70 @@ __device__ __forceinline__ float split_term(float x, float m) {
 }
 
 struct Scratch {
-  float cand[kCap];
-  uint32_t hist[2][256];
+  alignas(16) float cand[kCap];
+  alignas(16) uint32_t hist[3][256];
   double red_d[2][kWaves];
   int64_t red_i[kWaves];
   float red_f[kWaves];
   int red_flag[kWaves];
-  uint32_t digit[2];
-  int64_t rank[2];
 };
 
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
 __device__ __forceinline__ int wave_id() { return static_cast<int>(threadIdx.x) / kWave; }
 
-// Workgroup sum of `count`, OR of `flag` and max of `v` in one exchange (two barriers).
-__device__ void group_reduce(int64_t& count, int& flag, float& v, Scratch& s) {
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off /= 2) {
-    count += __shfl_xor(count, off, kWave);
-    flag |= __shfl_xor(flag, off, kWave);
-    v = fmaxf(v, __shfl_xor(v, off, kWave));
-  }
+// The value of v in the lane kCtrl's DPP pattern names (every lane has a source here).
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, 0xF, 0xF, false));
+}
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __uint_as_float(dpp<kCtrl>(__float_as_uint(v)));
+}
+template <int kCtrl>
+__device__ __forceinline__ double dpp(double v) {
+  const uint64_t u = static_cast<uint64_t>(__double_as_longlong(v));
+  const uint64_t lo = dpp<kCtrl>(static_cast<uint32_t>(u));
+  const uint64_t hi = dpp<kCtrl>(static_cast<uint32_t>(u >> 32));
+  return __longlong_as_double(static_cast<long long>(lo | (hi << 32)));
+}
+
+__device__ __forceinline__ uint32_t read_lane(uint32_t v, int lane) {
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), lane));
+}
+__device__ __forceinline__ float read_lane(float v, int lane) {
+  return __uint_as_float(read_lane(__float_as_uint(v), lane));
+}
+__device__ __forceinline__ double read_lane(double v, int lane) {
+  const uint64_t u = static_cast<uint64_t>(__double_as_longlong(v));
+  const uint64_t lo = read_lane(static_cast<uint32_t>(u), lane);
+  const uint64_t hi = read_lane(static_cast<uint32_t>(u >> 32), lane);
+  return __longlong_as_double(static_cast<long long>(lo | (hi << 32)));
+}
+
+// op over the wave's 64 lanes, the same value in every lane and a fixed order: a butterfly
+// inside each 16-lane row (quad_perm [1,0,3,2], [2,3,0,1], row_ror 4, row_ror 8), then the
+// four row results as (r0 op r1) op (r2 op r3).  Every lane must be active.
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_reduce(T v, Op op) {
+  v = op(v, dpp<0xB1>(v));
+  v = op(v, dpp<0x4E>(v));
+  v = op(v, dpp<0x124>(v));
+  v = op(v, dpp<0x128>(v));
+  return op(op(read_lane(v, 0), read_lane(v, 16)), op(read_lane(v, 32), read_lane(v, 48)));
+}
+
+// Workgroup sum of `count`, OR of `flag` and max of `v` (one barrier; the exchange slots are
+// not reused afterwards).  A lane's count and the wave's sum fit in 32 bits.
+__device__ void group_reduce(uint32_t lane_count, int64_t& count, int& flag, float& v, Scratch& s) {
+  const uint32_t c = wave_reduce(lane_count, [](uint32_t x, uint32_t y) { return x + y; });
+  const uint32_t f = wave_reduce(static_cast<uint32_t>(flag), [](uint32_t x, uint32_t y) { return x | y; });
+  const float mx = wave_reduce(v, [](float x, float y) { return fmaxf(x, y); });
   if (lane_id() == 0) {
-    s.red_i[wave_id()] = count;
-    s.red_flag[wave_id()] = flag;
-    s.red_f[wave_id()] = v;
+    s.red_i[wave_id()] = c;
+    s.red_flag[wave_id()] = static_cast<int>(f);
+    s.red_f[wave_id()] = mx;
   }
   __syncthreads();
   count = 0;
@@ -118,16 +157,14 @@ __device__ void group_reduce(int64_t& count, int& flag, float& v, Scratch& s) {
     flag |= s.red_flag[w];
     v = fmaxf(v, s.red_f[w]);
   }
-  __syncthreads();
 }
 
-// Two FP64 sums at once (the kept mass and the mass above the token).
+// Two FP64 sums at once (the kept mass and the mass above the token), in a fixed order (one
+// barrier; the exchange slots are not reused afterwards).
 __device__ void group_sum2(double& a, double& b, Scratch& s) {
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off /= 2) {
-    a += __shfl_xor(a, off, kWave);
-    b += __shfl_xor(b, off, kWave);
-  }
+  const auto add = [](double x, double y) { return x + y; };
+  a = wave_reduce(a, add);
+  b = wave_reduce(b, add);
   if (lane_id() == 0) {
     s.red_d[0][wave_id()] = a;
     s.red_d[1][wave_id()] = b;
@@ -140,7 +177,6 @@ __device__ void group_sum2(double& a, double& b, Scratch& s) {
     a += s.red_d[0][w];
     b += s.red_d[1][w];
   }
-  __syncthreads();
 }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -221,75 +257,66 @@ __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
   return static_cast<uint32_t>(a);
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 // Key of the rank-th largest (1-based) of the workgroup's keys, by an exact radix select over
-// 8-bit digits with an LDS histogram.  visit(f) calls f(key) for each key a lane holds, in
-// the same way on every round (each key by one lane).  Every lane returns the same key.  With
-// kRounds < 4 only the top 8 kRounds bits are selected and the rest are zero: the result is
-// the smallest key of the bucket that holds the rank-th largest.
+// 8-bit digits with LDS histograms.  visit(f) calls f(key) for each key a lane holds, the same
+// way on every round (each key by one lane).  Every lane returns the same key.  With kRounds < 4
+// only the top 8 kRounds bits are selected and the rest are zero: the result is the smallest key
+// of the bucket that holds the rank-th largest.  The caller clears hist[0], with a barrier
+// between that and the call.
 template <int kRounds = 4, typename V>
 __device__ uint32_t radix_select(int64_t rank, V&& visit, Scratch& s) {
   const int t = static_cast<int>(threadIdx.x);
+  const int l = lane_id();
   uint32_t prefix = 0;
   uint32_t mask = 0;
-  // Round r counts into hist[r % 2] and publishes digit[r % 2] / rank[r % 2]; the other
-  // buffer is cleared meanwhile (its last reader finished before the previous barrier), so a
-  // round needs two barriers.
-  if (t < 256) {
-    s.hist[0][t] = 0;
-    s.hist[1][t] = 0;
-  }
-  __syncthreads();
+  uint32_t want = static_cast<uint32_t>(rank);  // counts fit in 32 bits (vocab < 2^31)
 #pragma unroll
   for (int round = 0; round < kRounds; ++round) {
     const int shift = 24 - 8 * round;
-    const int cur = round & 1;
-    if (round > 0 && t < 256) s.hist[cur ^ 1][t] = 0;
+    uint32_t* const hist = s.hist[round % 3];
+    // Round r counts into hist[r % 3] and clears hist[(r + 1) % 3], last read by the scans of
+    // round r - 2, which every wave finished before the barrier of round r - 1; every wave
+    // scans the histogram itself, so a round takes one barrier.
+    if (t < 256) s.hist[(round + 1) % 3][t] = 0;
     visit([&](uint32_t k) {
       const bool hit = (k & mask) == prefix;
       const uint32_t digit = (k >> shift) & 255u;
       // Keys bunch into a few buckets (one exponent byte for every candidate): a wave whose
       // counted lanes share one digit adds them with one atomic instead of serialising them.
       const uint64_t counted = __ballot(hit);
-      const uint32_t d0 = __shfl(digit, counted ? __builtin_ctzll(counted) : 0, kWave);
+      const int first = counted ? __builtin_ctzll(counted) : 0;
+      const uint32_t d0 = read_lane(digit, first);
       if (__ballot(hit && digit != d0) == 0) {
-        if (counted != 0 && lane_id() == __builtin_ctzll(counted))
-          atomicAdd(&s.hist[cur][d0], static_cast<uint32_t>(__builtin_popcountll(counted)));
+        if (counted != 0 && l == first)
+          atomicAdd(&hist[d0], static_cast<uint32_t>(__builtin_popcountll(counted)));
       } else if (hit) {
-        atomicAdd(&s.hist[cur][digit], 1u);
+        atomicAdd(&hist[digit], 1u);
       }
     });
     __syncthreads();
-    if (wave_id() == 0) {
-      // lane l owns digits 255 - 4l ... 252 - 4l (descending); scan lanes in order
-      // counts fit in 32 bits (the host limits vocab to 2^31 - 1)
-      const int l = lane_id();
-      const uint32_t want = static_cast<uint32_t>(rank);
-      uint32_t h[4];
-      uint32_t own = 0;
+    // lane l owns digits 255 - 4l ... 252 - 4l (descending); h[3] is digit 255 - 4l
+    const u32x4 h = *reinterpret_cast<const u32x4*>(hist + 252 - 4 * l);
+    const uint32_t own = h[0] + h[1] + h[2] + h[3];
+    const uint32_t incl = wave_inclusive_sum(own);
+    uint32_t cum = incl - own;
+    uint32_t lane_digit = 0;
+    uint32_t lane_rank = 0;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        h[q] = s.hist[cur][255 - 4 * l - q];
-        own += h[q];
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t hq = h[3 - q];
+      if (cum < want && want <= cum + hq) {
+        lane_digit = static_cast<uint32_t>(255 - 4 * l - q);
+        lane_rank = want - cum;
       }
-      const uint32_t incl = wave_inclusive_sum(own);
-      const uint32_t excl = incl - own;
-      if (excl < want && want <= incl) {
-        uint32_t cum = excl;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (cum + h[q] >= want) {
-            s.digit[cur] = static_cast<uint32_t>(255 - 4 * l - q);
-            s.rank[cur] = want - cum;
-            break;
-          }
-          cum += h[q];
-        }
-      }
+      cum += hq;
     }
-    __syncthreads();
-    prefix |= s.digit[cur] << shift;
+    const uint64_t owner = __ballot(lane_rank != 0);
+    const int src = owner ? __builtin_ctzll(owner) : 0;
+    prefix |= read_lane(lane_digit, src) << shift;
     mask |= 255u << shift;
-    rank = s.rank[cur];
+    want = read_lane(lane_rank, src);
   }
   return prefix;
 }
@@ -354,6 +381,8 @@ __global__ void __launch_bounds__(kThreads) member_kernel(const MemberArgs A) {
   float low = -__builtin_inff();
   auto threshold = [&] {
     const uint32_t key = order_key(lane_max);
+    if (t < 256) s.hist[0][t] = 0;
+    __syncthreads();
     low = key_value(radix_select<2>(k_eff, [&](auto&& f) { f(key); }, s));
     if (low != low) low = -__builtin_inff();
   };
@@ -407,10 +436,13 @@ __global__ void __launch_bounds__(kThreads) member_kernel(const MemberArgs A) {
   // bit 0: a NaN in the row; bit 1: a wave's segment overflowed (every lane runs here, so the
   // first active lane is lane 0)
   wcount = __builtin_amdgcn_readfirstlane(wcount);
-  int64_t above = above_lane;
+  int64_t above = 0;
   int flags = nan | (wcount > kSeg ? 2 : 0);
   float m = lane_max;
-  group_reduce(above, flags, m, s);
+  // hist[0] is cleared for the select below; its last readers (the threshold's first round)
+  // are done, and the barrier of group_reduce orders the clear before the select
+  if (t < 256) s.hist[0][t] = 0;
+  group_reduce(above_lane, above, flags, m, s);
   const bool any_nan = flags & 1;
   const bool overflow = flags & 2;
 
