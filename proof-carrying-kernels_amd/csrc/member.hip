@@ -259,6 +259,51 @@ __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Adds the digits (k >> shift) & 255 of the keys with (k & mask) == prefix into hist.  Keys
+// bunch into a few buckets (one exponent byte for every candidate): a wave whose counted lanes
+// share one digit adds them with one atomic instead of serialising them.
+__device__ __forceinline__ void radix_count(uint32_t k, uint32_t prefix, uint32_t mask,
+                                            int shift, uint32_t* hist) {
+  const bool hit = (k & mask) == prefix;
+  const uint32_t digit = (k >> shift) & 255u;
+  const uint64_t counted = __ballot(hit);
+  const int first = counted ? __builtin_ctzll(counted) : 0;
+  const uint32_t d0 = read_lane(digit, first);
+  if (__ballot(hit && digit != d0) == 0) {
+    if (counted != 0 && lane_id() == first)
+      atomicAdd(&hist[d0], static_cast<uint32_t>(__builtin_popcountll(counted)));
+  } else if (hit) {
+    atomicAdd(&hist[digit], 1u);
+  }
+}
+
+// The digit of a complete 256-bin histogram that holds the want-th largest key, with want
+// turned into the rank within that digit; every wave computes it itself.  Lane l owns digits
+// 255 - 4l ... 252 - 4l (descending; h[3] is digit 255 - 4l).  The first lane whose inclusive
+// count reaches want owns the digit; its four counts and the count before them are read into
+// scalar registers and the descent runs once per wave.
+__device__ __forceinline__ uint32_t radix_find(const uint32_t* hist, uint32_t& want) {
+  const u32x4 h = *reinterpret_cast<const u32x4*>(hist + 252 - 4 * lane_id());
+  const uint32_t own = h[0] + h[1] + h[2] + h[3];
+  const uint32_t incl = wave_inclusive_sum(own);
+  const uint64_t reach = __ballot(incl >= want);
+  const int src = reach ? __builtin_ctzll(reach) : kWave - 1;
+  uint32_t rest = want - read_lane(incl - own, src);  // rank within the owner's four digits
+  uint32_t digit = static_cast<uint32_t>(255 - 4 * src);
+  const uint32_t c3 = read_lane(h[3], src);
+  const uint32_t c2 = read_lane(h[2], src);
+  const uint32_t c1 = read_lane(h[1], src);
+  if (rest > c3) {
+    rest -= c3, --digit;
+    if (rest > c2) {
+      rest -= c2, --digit;
+      if (rest > c1) rest -= c1, --digit;
+    }
+  }
+  want = rest;
+  return digit;
+}
+
 // Key of the rank-th largest (1-based) of the workgroup's keys, by an exact radix select over
 // 8-bit digits with LDS histograms.  visit(f) calls f(key) for each key a lane holds, the same
 // way on every round (each key by one lane).  Every lane returns the same key.  With kRounds < 4
@@ -268,7 +313,6 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 template <int kRounds = 4, typename V>
 __device__ uint32_t radix_select(int64_t rank, V&& visit, Scratch& s) {
   const int t = static_cast<int>(threadIdx.x);
-  const int l = lane_id();
   uint32_t prefix = 0;
   uint32_t mask = 0;
   uint32_t want = static_cast<uint32_t>(rank);  // counts fit in 32 bits (vocab < 2^31)
@@ -280,43 +324,10 @@ __device__ uint32_t radix_select(int64_t rank, V&& visit, Scratch& s) {
     // round r - 2, which every wave finished before the barrier of round r - 1; every wave
     // scans the histogram itself, so a round takes one barrier.
     if (t < 256) s.hist[(round + 1) % 3][t] = 0;
-    visit([&](uint32_t k) {
-      const bool hit = (k & mask) == prefix;
-      const uint32_t digit = (k >> shift) & 255u;
-      // Keys bunch into a few buckets (one exponent byte for every candidate): a wave whose
-      // counted lanes share one digit adds them with one atomic instead of serialising them.
-      const uint64_t counted = __ballot(hit);
-      const int first = counted ? __builtin_ctzll(counted) : 0;
-      const uint32_t d0 = read_lane(digit, first);
-      if (__ballot(hit && digit != d0) == 0) {
-        if (counted != 0 && l == first)
-          atomicAdd(&hist[d0], static_cast<uint32_t>(__builtin_popcountll(counted)));
-      } else if (hit) {
-        atomicAdd(&hist[digit], 1u);
-      }
-    });
+    visit([&](uint32_t k) { radix_count(k, prefix, mask, shift, hist); });
     __syncthreads();
-    // lane l owns digits 255 - 4l ... 252 - 4l (descending); h[3] is digit 255 - 4l
-    const u32x4 h = *reinterpret_cast<const u32x4*>(hist + 252 - 4 * l);
-    const uint32_t own = h[0] + h[1] + h[2] + h[3];
-    const uint32_t incl = wave_inclusive_sum(own);
-    uint32_t cum = incl - own;
-    uint32_t lane_digit = 0;
-    uint32_t lane_rank = 0;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t hq = h[3 - q];
-      if (cum < want && want <= cum + hq) {
-        lane_digit = static_cast<uint32_t>(255 - 4 * l - q);
-        lane_rank = want - cum;
-      }
-      cum += hq;
-    }
-    const uint64_t owner = __ballot(lane_rank != 0);
-    const int src = owner ? __builtin_ctzll(owner) : 0;
-    prefix |= read_lane(lane_digit, src) << shift;
+    prefix |= radix_find(hist, want) << shift;
     mask |= 255u << shift;
-    want = read_lane(lane_rank, src);
   }
   return prefix;
 }
@@ -397,13 +408,13 @@ __global__ void __launch_bounds__(kThreads) member_kernel(const MemberArgs A) {
     const bool take = l >= low;
     const uint64_t want = __ballot(take);
     if (want != 0) {
-      const int base = __builtin_amdgcn_readfirstlane(wcount);
+      const int first = __builtin_amdgcn_readfirstlane(wcount);
       if (take) {
         const uint64_t below = lane_id() ? want & (~0ull >> (kWave - lane_id())) : 0ull;
-        const int at = base + __builtin_popcountll(below);
+        const int at = first + __builtin_popcountll(below);
         if (at < kSeg) seg[at] = l;
       }
-      wcount = base + __builtin_popcountll(want);
+      wcount = first + __builtin_popcountll(want);
     }
   };
   // Most quads hold no candidate: one ballot per quad decides whether any lane needs compact.
@@ -433,11 +444,11 @@ __global__ void __launch_bounds__(kThreads) member_kernel(const MemberArgs A) {
   } else {
     for_each<true>(row, prefix, vocab, scan);
   }
-  // bit 0: a NaN in the row; bit 1: a wave's segment overflowed (every lane runs here, so the
-  // first active lane is lane 0)
+  // bit 0: a NaN in the row; bit 1: a wave's segment overflowed; bit 2: a wave holds more
+  // candidates than lanes (every lane runs here, so the first active lane is lane 0)
   wcount = __builtin_amdgcn_readfirstlane(wcount);
   int64_t above = 0;
-  int flags = nan | (wcount > kSeg ? 2 : 0);
+  int flags = nan | (wcount > kSeg ? 2 : 0) | (wcount > kWave ? 4 : 0);
   float m = lane_max;
   // hist[0] is cleared for the select below; its last readers (the threshold's first round)
   // are done, and the barrier of group_reduce orders the clear before the select
@@ -457,6 +468,20 @@ __global__ void __launch_bounds__(kThreads) member_kernel(const MemberArgs A) {
         z += e;
         a += l > lt ? e : 0.0;
       });
+    } else if (fused && !(flags & 4)) {
+      // At most one candidate per lane (the common case): each lane keeps its candidate, key
+      // and term in registers for every round of the select.
+      const bool have = lane_id() < wcount;
+      const float c = have ? seg[lane_id()] : 0.0f;
+      const uint32_t key = order_key(c);
+      const float e = have ? split_term(c, m) : 0.0f;
+      const float kth = key_value(radix_select(k_eff, [&](auto&& f) {
+        if (have) f(key);
+      }, s));
+      if (have && c >= kth) {
+        z = e;
+        a = c > lt ? e : 0.0;
+      }
     } else if (fused && !overflow) {
       // each wave reads back its own segment (LDS is in order within a wave)
       const float kth = key_value(radix_select(k_eff, [&](auto&& f) {

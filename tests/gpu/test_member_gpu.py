@@ -109,23 +109,31 @@ def test_nan_rows_reject() -> None:
 
 
 CASES = ["all_equal", "many_ties", "k_above_1024", "keep_all_rows", "mixed", "k_700",
-         "one_wave_overflows"]  # fmt: skip
+         "k_700_offset", "one_wave_overflows", "wide_window"]  # fmt: skip
 
 
 @pytest.mark.parametrize("case", CASES)
 def test_fallback_paths_match_the_oracle(case: str) -> None:
-    """Rows whose candidate set overflows LDS, k_eff above 1024, rows without top-k; k_700
-    leaves ~1400 candidates (several per lane of each wave's segment, none overflowing) and
-    one_wave_overflows puts 512 equal maxima in the stream slots of one wave only (that wave's
-    segment overflows while the row's total fits)."""
+    """Rows whose candidate set overflows LDS, k_eff above 1024, rows without top-k.  k_700 and
+    k_700_offset leave ~1400 candidates (several per lane of each wave's segment, none
+    overflowing), spread over four binades or packed into one.  one_wave_overflows puts 512
+    equal maxima in the stream slots of one wave only (that wave's segment overflows while the
+    row's total fits).  wide_window plants three huge logits per row among ordinary candidates
+    (rows with top-k 50 hold at most one candidate per lane, rows with 700 several)."""
     rng = np.random.default_rng(5)
     rows, vocab = 8, 20000
     if case == "one_wave_overflows":
         rows, vocab = 2, 151_936
     logits = (rng.standard_normal((rows, vocab)) * 2).astype(np.float32)
     top_k = np.full(rows, 50)
-    if case == "k_700":
+    if case in ("k_700", "k_700_offset"):
         top_k[:] = 700
+        if case == "k_700_offset":
+            logits += 100.0
+    elif case == "wide_window":
+        for r in range(rows):
+            logits[r, rng.choice(vocab, 3, replace=False)] = [1e20, 3e10, 7e5]
+        top_k[rows // 2 :] = 700
     elif case == "one_wave_overflows":
         # the stream starts at logit 16384; lane t of the workgroup reads quad 4096 + t +
         # 1024 j, so wave 3 (lanes 192..255) reads logits 16384 + 4096 j + 768 .. + 1023
