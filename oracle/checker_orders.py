@@ -35,8 +35,9 @@ and differ only in how they round on the way.
   - a_j |x_j| exact in FP64, added upward;
 - the remaining columns j (all of them when n % 4 != 0) go into accumulator j % 4;
 - the four accumulators combine as (0 + 2) + (1 + 3);
-- the lanes combine by a 64-lane butterfly, which gives lane 0 the halving order
-  (i += i + 32, ..., 1), and the four waves as (0 + 2) + (1 + 3);
+- the lanes combine by a 64-lane butterfly over lane distances 1, 2, 4, ..., 32, which gives
+  lane 0 the adjacent-pair tree ((v0 + v1) + (v2 + v3)) + ..., and the four waves as
+  (0 + 2) + (1 + 3);
 - s stays in FP64 (+inf beyond the FP32 range), and tau is formed with `rounding.h`'s mul_up
   and add_up, including mul_up's one-ulp raise of a nonzero product below 2^-960.
 
@@ -136,6 +137,14 @@ def _halve(v: F64, width: int, up: bool) -> F64:
         lo, hi = v[..., :off], v[..., off : 2 * off]
         v[..., :off] = add_up64(lo, hi) if up else lo + hi
         off //= 2
+    return v[..., 0]
+
+
+def _pairs_up(v: F64, up: bool) -> F64:
+    """Adjacent-pair tree over the last axis (a power of two): ((v0 + v1) + (v2 + v3)) + ...,
+    lane 0's result of a butterfly over distances 1, 2, 4, ..."""
+    while v.shape[-1] > 1:
+        v = add_up64(v[..., 0::2], v[..., 1::2]) if up else v[..., 0::2] + v[..., 1::2]
     return v[..., 0]
 
 
@@ -288,7 +297,7 @@ def hip_check(c, a, r, x, y, coef: float, geps: float, tau_floor: float  # type:
     q_s = add_up64(add_up64(sa[0], sa[2]), add_up64(sa[1], sa[3]))
 
     def group(v: F64, up: bool) -> F64:
-        waves = _halve(v.reshape(P, THREADS // WAVE, WAVE), WAVE, up)  # (P, 4)
+        waves = _pairs_up(v.reshape(P, THREADS // WAVE, WAVE), up)  # (P, 4)
         add = add_up64 if up else (lambda u, w: u + w)
         return add(add(waves[:, 0], waves[:, 2]), add(waves[:, 1], waves[:, 3]))
 

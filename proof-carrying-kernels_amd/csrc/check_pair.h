@@ -27,8 +27,9 @@
 //
 // Order.  Lane t accumulates the y terms of rows t, t + 256, ..., then the bank quads t,
 // t + 256, t + 512, ... in increasing order (four accumulators per quantity, one per column of a
-// quad); the workgroup reduction is a fixed wave64 butterfly and a fixed halving over the four
-// waves.  The result does not depend on scheduling or on kAhead (loads issued ahead per lane).
+// quad); the workgroup reduction is a fixed wave64 butterfly over lane distances 1, 2, 4, 8, 16,
+// 32 (so lane 0 holds ((v0 + v1) + (v2 + v3)) + ...) and a fixed halving over the four waves.
+// The result does not depend on scheduling or on kAhead (loads issued ahead per lane).
 
 #pragma once
 
@@ -84,14 +85,44 @@ __device__ __forceinline__ Quad combine(const Quad& a, const Quad& b) {
   return Quad{a.cx + b.cx, add_up_nonneg(a.s, b.s), a.ry + b.ry, add_up_nonneg(a.yabs, b.yabs)};
 }
 
-// Workgroup sums of the four quantities in one exchange, valid in every lane.
+// v in the lane that DPP pattern kCtrl names (every lane has a source for the patterns used).
+template <int kCtrl>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t u = static_cast<uint64_t>(__double_as_longlong(v));
+  const uint64_t lo = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+      0, static_cast<int>(static_cast<uint32_t>(u)), kCtrl, 0xF, 0xF, false));
+  const uint64_t hi = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+      0, static_cast<int>(static_cast<uint32_t>(u >> 32)), kCtrl, 0xF, 0xF, false));
+  return __longlong_as_double(static_cast<long long>(lo | (hi << 32)));
+}
+template <int kCtrl>
+__device__ __forceinline__ Quad dpp_quad(const Quad& v) {
+  return Quad{dpp_f64<kCtrl>(v.cx), dpp_f64<kCtrl>(v.s), dpp_f64<kCtrl>(v.ry), dpp_f64<kCtrl>(v.yabs)};
+}
+__device__ __forceinline__ double lane_f64(double v, int lane) {
+  const uint64_t u = static_cast<uint64_t>(__double_as_longlong(v));
+  const uint64_t lo = static_cast<uint32_t>(
+      __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(u)), lane));
+  const uint64_t hi = static_cast<uint32_t>(
+      __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(u >> 32)), lane));
+  return __longlong_as_double(static_cast<long long>(lo | (hi << 32)));
+}
+__device__ __forceinline__ Quad lane_quad(const Quad& v, int lane) {
+  return Quad{lane_f64(v.cx, lane), lane_f64(v.s, lane), lane_f64(v.ry, lane), lane_f64(v.yabs, lane)};
+}
+
+// Workgroup sums of the four quantities in one exchange, valid in every lane.  Inside each
+// 16-lane row the partners are the lanes at distance 1 and 2 (quad_perm), then the mirror lanes
+// in the other quad (row_half_mirror) and the other half-row (row_mirror); every lane of a group
+// holds the same value after each level (combine is symmetric in its operands), so this is the
+// butterfly over distances 1, 2, 4 and 8.  The rows then combine as (r0 + r1) + (r2 + r3),
+// the butterfly's distances 16 and 32, read from lanes 0, 16, 32 and 48.
 __device__ __forceinline__ Quad group_sum(Quad v, Quad* lds) {
-#pragma unroll
-  for (int off = kWave / 2; off > 0; off /= 2) {
-    const Quad o{__shfl_xor(v.cx, off, kWave), __shfl_xor(v.s, off, kWave),
-                 __shfl_xor(v.ry, off, kWave), __shfl_xor(v.yabs, off, kWave)};
-    v = combine(v, o);  // symmetric in its operands: every lane holds the same value
-  }
+  v = combine(v, dpp_quad<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+  v = combine(v, dpp_quad<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+  v = combine(v, dpp_quad<0x141>(v));  // row_half_mirror
+  v = combine(v, dpp_quad<0x140>(v));  // row_mirror
+  v = combine(combine(lane_quad(v, 0), lane_quad(v, 16)), combine(lane_quad(v, 32), lane_quad(v, 48)));
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   if ((threadIdx.x & (kWave - 1)) == 0) lds[wave] = v;
   __syncthreads();
@@ -111,12 +142,21 @@ __device__ __forceinline__ void column(double& cx, double& s, double cj, double 
   s = add_up_nonneg(s, aj * __builtin_fabs(xj));
 }
 
-// Checks work item `item` of `batch` (one (check, block) pair) with the calling workgroup of
-// kThreads lanes; `lds` holds kWaves Quads.  Lane 0 writes passed, rho and tau.
-template <int kAhead>
-__device__ __forceinline__ void check_pair(const PckCheckBatch& batch, int64_t item, Quad* lds) {
+// The descriptor that owns work item `item`: the number of boundaries start[1 .. count - 1]
+// at or below it (start increases), from independent loads rather than a chain of them.
+__device__ __forceinline__ int owner(const PckCheckBatch& batch, int64_t item) {
   int g = 0;
-  while (g + 1 < batch.count && item >= batch.start[g + 1]) ++g;
+#pragma unroll
+  for (int j = 1; j < PCK_MAX_BATCH; ++j) g += (j < batch.count && item >= batch.start[j]) ? 1 : 0;
+  return g;
+}
+
+// Checks work item `item` of `batch` (one (check, block) pair, owned by descriptor g) with the
+// calling workgroup of kThreads lanes; `lds` holds kWaves Quads.  Lane 0 writes passed, rho and
+// tau.
+template <int kAhead>
+__device__ __forceinline__ void check_pair(const PckCheckBatch& batch, int64_t item, int g,
+                                           Quad* lds) {
   const PckCheckDesc& d = batch.desc[g];
   const int64_t pair = item - batch.start[g];  // k * num_blocks + beta
   const int64_t beta = pair % d.num_blocks;
@@ -128,13 +168,22 @@ __device__ __forceinline__ void check_pair(const PckCheckBatch& batch, int64_t i
   const int8_t* r_row = d.r + pair * d.block;
   const float* y_blk = d.y + beta * d.block;
 
-  // The y terms first: their loads are independent of the bank's.  A non-finite y makes
-  // sum |y| non-finite (FP32 values cannot overflow an FP64 sum of at most 2^31 of them).
+  // The y terms.  A block of at most kThreads rows is one value per lane, requested here with
+  // unconditional loads (row 0 for lanes past the block, dropped at use: a branch around the
+  // loads would make its merge wait for them) and used after the bank's loads are issued;
+  // longer blocks loop.  A non-finite y makes sum |y| non-finite (FP32 values cannot overflow
+  // an FP64 sum of at most 2^31 of them).
   Quad q{0.0, 0.0, 0.0, 0.0};
-  for (int i = t; i < d.block; i += kThreads) {
-    const double yd = static_cast<double>(y_blk[i]);
-    q.ry = q.ry + (r_row[i] > 0 ? yd : -yd);
-    q.yabs = add_up_nonneg(q.yabs, __builtin_fabs(yd));
+  const bool one_y = d.block <= kThreads;
+  const int yi = t < d.block ? t : 0;
+  const float y_mine = y_blk[yi];
+  const int8_t r_mine = r_row[yi];
+  if (!one_y) {
+    for (int i = t; i < d.block; i += kThreads) {
+      const double yd = static_cast<double>(y_blk[i]);
+      q.ry = q.ry + (r_row[i] > 0 ? yd : -yd);
+      q.yabs = add_up_nonneg(q.yabs, __builtin_fabs(yd));
+    }
   }
 
   // Bank terms: kAhead quads per lane are loaded before any is consumed; indices past the row
@@ -189,6 +238,11 @@ __device__ __forceinline__ void check_pair(const PckCheckBatch& batch, int64_t i
   for (int64_t j = done + t; j < n; j += kThreads) {
     column(cx[j & 3], sa[j & 3], static_cast<double>(c_row[j]), bf16_at(a_row, j), bf16_at(x, j));
   }
+  if (one_y && t < d.block) {
+    const double yd = static_cast<double>(y_mine);
+    q.ry = r_mine > 0 ? yd : -yd;
+    q.yabs = __builtin_fabs(yd);
+  }
   q.cx = (cx[0] + cx[2]) + (cx[1] + cx[3]);
   q.s = add_up_nonneg(add_up_nonneg(sa[0], sa[2]), add_up_nonneg(sa[1], sa[3]));
 
@@ -196,9 +250,18 @@ __device__ __forceinline__ void check_pair(const PckCheckBatch& batch, int64_t i
   if (t == 0) {
     const double s_up = within_f32_range(total.s);
     const double rho = total.cx - total.ry;
-    const double cabs_up = mul_up(kOnePlusU32, s_up);
-    const double eps = mul_up(d.geps, add_up(cabs_up, total.yabs));
-    const double tau = add_up(add_up(mul_up(d.coef, s_up), eps), d.tau_floor);
+    double tau;
+    if (d.coef >= 0.0 && d.geps >= 0.0 && d.tau_floor >= 0.0) {
+      // every operand is >= +0 (or +inf / NaN), where these branch-free forms give the
+      // general operations' results
+      const double cabs_up = mul_up_pos(kOnePlusU32, s_up);
+      const double eps = mul_up_pos(d.geps, add_up_nonneg(cabs_up, total.yabs));
+      tau = add_up_nonneg(add_up_nonneg(mul_up_pos(d.coef, s_up), eps), d.tau_floor);
+    } else {
+      const double cabs_up = mul_up(kOnePlusU32, s_up);
+      const double eps = mul_up(d.geps, add_up(cabs_up, total.yabs));
+      tau = add_up(add_up(mul_up(d.coef, s_up), eps), d.tau_floor);
+    }
     // Non-finite outputs and an overflowing threshold (tau = inf) fail closed; NaN compares
     // false.
     d.passed[pair] =

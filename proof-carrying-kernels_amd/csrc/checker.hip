@@ -28,7 +28,14 @@ namespace {
 
 __global__ void __launch_bounds__(check::kThreads) blocked_check_kernel(const PckCheckBatch batch) {
   __shared__ check::Quad lds[check::kWaves];
-  check::check_pair<8>(batch, blockIdx.x, lds);
+  const int64_t item = blockIdx.x;
+  const int g = check::owner(batch, item);
+  // Rows of more than 8 quads per lane keep 16 in flight (one round trip for n up to 16 K);
+  // the order, and so every bit, is the same for any number in flight.
+  if (batch.desc[g].n > 8 * 4 * check::kThreads)
+    check::check_pair<16>(batch, item, g, lds);
+  else
+    check::check_pair<8>(batch, item, g, lds);
 }
 
 constexpr int kRowSumWaves = 4;

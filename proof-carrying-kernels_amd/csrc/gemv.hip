@@ -371,7 +371,7 @@ __global__ void __launch_bounds__(kGroupThreads)
   __shared__ check::Quad lds[check::kWaves];
   const int64_t items = ride.start[ride.count];
   if (static_cast<int64_t>(blockIdx.x) < items) {
-    check::check_pair<4>(ride, blockIdx.x, lds);
+    check::check_pair<4>(ride, blockIdx.x, check::owner(ride, blockIdx.x), lds);
     return;
   }
   gemv_rows<T, R, U, kFp8, true, kPad, kNt>(batch, static_cast<int64_t>(blockIdx.x) - items);

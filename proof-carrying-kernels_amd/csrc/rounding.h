@@ -72,6 +72,18 @@ __device__ __forceinline__ double add_up_nonneg(double a, double b) {
   return err > 0.0 ? raised : s;
 }
 
+// mul_up(a, b) for a, b >= +0 without branches, with the same result there: a zero factor
+// keeps +0; a product of nonzero factors below 2^-960 (an underflow to 0 included) is raised
+// one ulp from its round-to-nearest value, any other when the FMA residual is positive; +inf
+// and NaN pass through (their residual is NaN).
+__device__ __forceinline__ double mul_up_pos(double a, double b) {
+  const double p = a * b;
+  const double err = __builtin_fma(a, b, -p);
+  const bool tiny = p < 0x1p-960 && a != 0.0 && b != 0.0;
+  const double raised = __longlong_as_double(__double_as_longlong(p) + 1);
+  return (err > 0.0 || tiny) ? raised : p;
+}
+
 // RU(a b) for a, b >= 0 without branches: raised by one ulp when the FMA residual is positive
 // or the product is below 2^-960 (where the residual may be inexact; raising still bounds a b
 // from above); +inf stays +inf (its residual is -inf or NaN) and NaN stays NaN.

@@ -423,3 +423,27 @@ def test_passed_rho_tau_equal_the_hip_model_bit_for_bit(m: int, n: int, block: i
         finite = np.isfinite(tau_ref)
         assert (res.tau.cpu().numpy()[finite] <= tau_ref[finite]).all(), name
     assert bool(check_many([(ch, xt, y)])[0].passed.all())
+
+
+def test_zero_activations_give_the_model_bits() -> None:
+    """x = 0 (and zero weight rows with a nonzero x) leave s = 0: tau is the threshold's floor
+    terms only, with the exact zero products kept at +0 (no ulp raise), bit for bit as the
+    model's general round-up product gives them."""
+    from oracle.checker_orders import hip_check
+
+    m, n, block = 256, 4096, 128
+    W, x, Wt, xt = problem(m, n, seed=11)
+    W[:block] = 0.0  # first block: zero rows
+    Wt = torch.from_numpy(W).to(torch.bfloat16).cuda()
+    ch = GpuBlockedChecker(Wt, block, tree_height(n, THREADS, 8), checks=2,
+                           generator=torch.Generator().manual_seed(1))  # fmt: skip
+    c, a, r = ch.c.cpu().numpy(), ch.a.float().cpu().numpy(), ch.r.cpu().numpy()
+    for xv in (np.zeros_like(x), x):
+        xg = torch.from_numpy(xv).to(torch.bfloat16).cuda()
+        y = gemv_coalesced(Wt, xg, THREADS)
+        res = check_many([(ch, xg, y)])[0]
+        passed, rho, tau = hip_check(c, a, r, xv, y.cpu().numpy(), ch.coef, ch.geps, ch.tau_floor)
+        assert np.array_equal(res.passed.cpu().numpy(), passed)
+        assert np.array_equal(res.tau.cpu().numpy().view(np.uint64), tau.view(np.uint64))
+        assert np.array_equal(res.rho.cpu().numpy().view(np.uint64), rho.view(np.uint64))
+        assert bool(res.passed.all())
