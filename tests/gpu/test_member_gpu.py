@@ -158,6 +158,25 @@ def test_fallback_paths_match_the_oracle(case: str) -> None:
     assert_matches_oracle(logits, tokens, top_k, top_p, top_k_host=top_k)
 
 
+@pytest.mark.parametrize("vocab", [20001, 20003, 151937])
+def test_odd_vocab_rows_take_every_alignment(vocab: int) -> None:
+    """With an odd vocab the rows start at every 4-byte offset: aligned rows end in an
+    element tail, the others stream element by element with lanes dropping out at the end of
+    each range (the per-wave candidate counts must survive both), and short prefixes are
+    re-read from memory.  Top-k + top-p rows (the candidate path) and rows without a top-k."""
+    rng = np.random.default_rng(vocab)
+    rows = 8
+    logits = (rng.standard_normal((rows, vocab)) * 3).astype(np.float32)
+    hot = rng.integers(0, vocab, (rows, 6))
+    logits[np.arange(rows)[:, None], hot] += 12.0
+    top_k = np.array([50, 50, 50, 50, 200, 700, vocab, 50])
+    order = np.argsort(-logits, axis=1, kind="stable")
+    tokens = order[np.arange(rows), rng.integers(0, 60, rows)]
+    top_p = np.full(rows, 0.9)
+    assert_matches_oracle(logits, tokens, top_k, top_p)
+    assert_matches_oracle(logits, tokens, top_k, top_p, top_k_host=top_k)
+
+
 def vllm_kept_row(row: np.ndarray, k: int, p: float) -> np.ndarray:
     """Token ids vLLM's own top-k then top-p masking keeps (apply_top_k_top_p_pytorch)."""
     order = np.argsort(row.astype(np.float64), kind="stable")
