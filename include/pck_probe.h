@@ -40,6 +40,12 @@ int pck_probe_mfma_bf16_16x16(const uint16_t* a, const uint16_t* b, const float*
 int pck_probe_mfma_bf16_k8(const uint16_t* a, const uint16_t* b, const float* c, float* d,
                            int64_t tiles, int steps, void* stream);
 
+/* The checkers' directed roundings (csrc/rounding.h) for n pairs: out[4 i .. 4 i + 3] =
+ * mul_up(a[i], b[i]), mul_up_pos(a[i], b[i]), add_up(a[i], b[i]), add_up_nonneg(a[i], b[i]).
+ * The branch-free forms are meant for non-negative operands, where they must give the
+ * general forms' bits. */
+int pck_probe_round_up(const double* a, const double* b, double* out, int64_t n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

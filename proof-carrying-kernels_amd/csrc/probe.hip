@@ -8,7 +8,8 @@
 //   pck_probe_mfma_bf16       v_mfma_f32_32x32x16_bf16 chains;
 //   pck_probe_mfma_bf16_k8    v_mfma_f32_32x32x8_bf16 chains (the batched product's step: one
 //                             group of 8 K-slots split over the two lane halves, 4 per lane);
-//   pck_probe_mfma_bf16_16x16 v_mfma_f32_16x16x32_bf16 chains (the batched checker's a . |x|).
+//   pck_probe_mfma_bf16_16x16 v_mfma_f32_16x16x32_bf16 chains (the batched checker's a . |x|);
+//   pck_probe_round_up        rounding.h's upward products and sums, general and branch-free.
 //
 // Operands are passed in lane order, so the probes embed no matrix layout: tile t, step s,
 // lane l reads its A and B operands at [(t * steps + s) * 64 + l] (8 or 4 BF16 values or one
@@ -21,6 +22,7 @@
 #include <cstdint>
 
 #include "pck_probe.h"
+#include "rounding.h"
 
 namespace {
 
@@ -93,6 +95,17 @@ __global__ void __launch_bounds__(kWave) mfma_bf16_k8_kernel(const uint16_t* a, 
   for (int v = 0; v < 16; ++v) d[(t * kWave + l) * 16 + v] = acc[v];
 }
 
+__global__ void __launch_bounds__(256) round_up_kernel(const double* a, const double* b,
+                                                       double* out, int64_t n) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+    out[4 * i] = pck::mul_up(a[i], b[i]);
+    out[4 * i + 1] = pck::mul_up_pos(a[i], b[i]);
+    out[4 * i + 2] = pck::add_up(a[i], b[i]);
+    out[4 * i + 3] = pck::add_up_nonneg(a[i], b[i]);
+  }
+}
+
 bool tiles_ok(int64_t tiles, int steps) {
   return tiles >= 1 && tiles <= (1 << 20) && steps >= 1 && steps <= 64;
 }
@@ -137,5 +150,16 @@ extern "C" int pck_probe_mfma_bf16_k8(const uint16_t* a, const uint16_t* b, cons
   if (!tiles_ok(tiles, steps) || !a || !b || !c || !d) return hipErrorInvalidValue;
   mfma_bf16_k8_kernel<<<dim3(static_cast<unsigned>(tiles)), dim3(kWave), 0,
                         static_cast<hipStream_t>(stream)>>>(a, b, c, d, steps);
+  return hipGetLastError();
+}
+
+extern "C" int pck_probe_round_up(const double* a, const double* b, double* out, int64_t n,
+                                  void* stream) {
+  if (n < 0 || (n > 0 && (a == nullptr || b == nullptr || out == nullptr)))
+    return hipErrorInvalidValue;
+  if (n == 0) return hipSuccess;
+  const int64_t blocks = (n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096;
+  round_up_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                    static_cast<hipStream_t>(stream)>>>(a, b, out, n);
   return hipGetLastError();
 }

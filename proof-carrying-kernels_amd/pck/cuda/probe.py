@@ -27,6 +27,7 @@ SIGNATURES = {
     "pck_probe_mfma_bf16": [_p, _p, _p, _p, _i64, _int, _p],
     "pck_probe_mfma_bf16_16x16": [_p, _p, _p, _p, _i64, _int, _p],
     "pck_probe_mfma_bf16_k8": [_p, _p, _p, _p, _i64, _int, _p],
+    "pck_probe_round_up": [_p, _p, _p, _i64, _p],
 }
 _handle: ctypes.CDLL | None = None
 
@@ -61,6 +62,18 @@ def expf(x: torch.Tensor) -> torch.Tensor:
         check(lib().pck_probe_expf(x.data_ptr(), y.data_ptr(), x.numel(), stream_handle(x.device)),
               "expf probe")  # fmt: skip
     return y
+
+
+def round_up(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """(n, 4) FP64: the device's mul_up, mul_up_pos, add_up and add_up_nonneg of the FP64 CUDA
+    tensors ``a`` and ``b`` (same shape, flattened)."""
+    a = _cuda(a, torch.float64, tuple(a.shape), "a")
+    b = _cuda(b, torch.float64, tuple(a.shape), "b")
+    out = torch.empty((a.numel(), 4), dtype=torch.float64, device=a.device)
+    with torch.cuda.device(a.device):
+        check(lib().pck_probe_round_up(a.data_ptr(), b.data_ptr(), out.data_ptr(), a.numel(),
+                                       stream_handle(a.device)), "round_up probe")  # fmt: skip
+    return out
 
 
 def _chain(name: str, a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, elems: int,

@@ -17,6 +17,10 @@ libpck_probe.so, built with the library's flags), against exact host arithmetic.
 - ``v_mfma_f32_16x16x32_bf16`` on non-negative operands (the batched checker's a . |x|): a
   step never falls below the exact sum by more than 2^-18 + 2^-24 relative (plus 33 x 2^-126),
   which the checker's round-up factor 1 + 2^-16 covers.
+- ``rounding.h``: on non-negative operands the branch-free mul_up_pos and add_up_nonneg give
+  the general mul_up and add_up bits (zeros, subnormals, products underflowing to 0 or below
+  2^-960, overflow, inf, NaN), and mul_up is the exact upward product except one ulp above it
+  for nonzero products below 2^-960.
 """
 
 from __future__ import annotations
@@ -219,3 +223,68 @@ def test_nonnegative_16x16x32_step_stays_within_the_checker_bound() -> None:
                 if ex > 0:
                     worst = max(worst, float((ex - got) / ex))
     print(f"largest relative shortfall of a non-negative step: {worst:.3e}", flush=True)
+
+
+def _special_nonneg() -> np.ndarray:
+    tiny = [0.0, 5e-324, 2.0**-1070, 2.0**-1022, np.nextafter(2.0**-960, 0), 2.0**-960,
+            np.nextafter(2.0**-960, 1), 2.0**-700, 2.0**-500, 1e-300]  # fmt: skip
+    mid = [2.0**-60, 0.1, 0.75, 1.0, 1.0 + 2.0**-52, 1.5, 3.0, 2.0**52 + 1, 1e100, 2.0**511]
+    big = [2.0**600, 1e308, np.finfo(np.float64).max, np.inf, np.nan]
+    return np.array(tiny + mid + big, dtype=np.float64)
+
+
+def _same_bits(x: np.ndarray, y: np.ndarray) -> np.ndarray:
+    return (x.view(np.uint64) == y.view(np.uint64)) | (np.isnan(x) & np.isnan(y))
+
+
+def test_branch_free_round_up_forms_equal_the_general_ones() -> None:
+    v = _special_nonneg()
+    a, b = (g.ravel() for g in np.meshgrid(v, v, indexing="ij"))
+    rng = np.random.default_rng(7)
+    ra = np.ldexp(rng.random(4096), rng.integers(-1100, 1000, 4096))
+    rb = np.ldexp(rng.random(4096), rng.integers(-1100, 1000, 4096))
+    a, b = np.concatenate([a, ra]), np.concatenate([b, rb])
+    out = probe.round_up(torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()).cpu().numpy()
+    print("round-up probe pairs", a.size, flush=True)
+    assert _same_bits(out[:, 0], out[:, 1]).all(), np.argwhere(~_same_bits(out[:, 0], out[:, 1]))[:4]
+    assert _same_bits(out[:, 2], out[:, 3]).all(), np.argwhere(~_same_bits(out[:, 2], out[:, 3]))[:4]
+    with np.errstate(over="ignore", under="ignore"):
+        _check_against_exact(a, b, out)
+
+
+def _check_against_exact(a: np.ndarray, b: np.ndarray, out: np.ndarray) -> None:
+    # mul_up against the exact upward product (finite operands)
+    for x, y, got in zip(a, b, out[:, 0]):
+        if not (np.isfinite(x) and np.isfinite(y)):
+            continue
+        rn = x * y
+        if not np.isfinite(rn):  # beyond the largest double: upward gives +inf
+            assert got == np.inf, (x, y, got)
+            continue
+        exact = Fraction(x) * Fraction(y)
+        ru = rn if Fraction(rn) >= exact else np.nextafter(rn, np.inf)
+        if exact != 0 and exact < Fraction(2) ** -960:
+            assert got in (ru, np.nextafter(ru, np.inf)), (x, y, got, ru)
+        else:
+            assert got == ru, (x, y, got, ru)
+    # add_up against the exact upward sum
+    for x, y, got in zip(a, b, out[:, 2]):
+        if not (np.isfinite(x) and np.isfinite(y)) or not np.isfinite(x + y):
+            continue
+        exact = Fraction(x) + Fraction(y)
+        rn = x + y
+        ru = rn if Fraction(rn) >= exact else np.nextafter(rn, np.inf)
+        assert got == ru, (x, y, got, ru)
+
+
+def test_general_round_up_forms_on_negative_operands() -> None:
+    """The general forms also round negative operands upward (the branch-free ones are not
+    used there)."""
+    rng = np.random.default_rng(8)
+    a = np.ldexp(rng.random(2048) - 0.5, rng.integers(-200, 200, 2048))
+    b = np.ldexp(rng.random(2048) - 0.5, rng.integers(-200, 200, 2048))
+    out = probe.round_up(torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()).cpu().numpy()
+    for x, y, mul, add in zip(a, b, out[:, 0], out[:, 2]):
+        for got, exact, rn in ((mul, Fraction(x) * Fraction(y), x * y), (add, Fraction(x) + Fraction(y), x + y)):
+            ru = rn if Fraction(rn) >= exact else np.nextafter(rn, np.inf)
+            assert got == ru, (x, y, got, ru)
