@@ -97,7 +97,8 @@ __device__ __forceinline__ double dpp_f64(double v) {
 }
 template <int kCtrl>
 __device__ __forceinline__ Quad dpp_quad(const Quad& v) {
-  return Quad{dpp_f64<kCtrl>(v.cx), dpp_f64<kCtrl>(v.s), dpp_f64<kCtrl>(v.ry), dpp_f64<kCtrl>(v.yabs)};
+  return Quad{dpp_f64<kCtrl>(v.cx), dpp_f64<kCtrl>(v.s), dpp_f64<kCtrl>(v.ry),
+              dpp_f64<kCtrl>(v.yabs)};
 }
 __device__ __forceinline__ double lane_f64(double v, int lane) {
   const uint64_t u = static_cast<uint64_t>(__double_as_longlong(v));
@@ -108,7 +109,8 @@ __device__ __forceinline__ double lane_f64(double v, int lane) {
   return __longlong_as_double(static_cast<long long>(lo | (hi << 32)));
 }
 __device__ __forceinline__ Quad lane_quad(const Quad& v, int lane) {
-  return Quad{lane_f64(v.cx, lane), lane_f64(v.s, lane), lane_f64(v.ry, lane), lane_f64(v.yabs, lane)};
+  return Quad{lane_f64(v.cx, lane), lane_f64(v.s, lane), lane_f64(v.ry, lane),
+              lane_f64(v.yabs, lane)};
 }
 
 // Workgroup sums of the four quantities in one exchange, valid in every lane.  Inside each
@@ -122,7 +124,8 @@ __device__ __forceinline__ Quad group_sum(Quad v, Quad* lds) {
   v = combine(v, dpp_quad<0x4E>(v));   // quad_perm [2, 3, 0, 1]
   v = combine(v, dpp_quad<0x141>(v));  // row_half_mirror
   v = combine(v, dpp_quad<0x140>(v));  // row_mirror
-  v = combine(combine(lane_quad(v, 0), lane_quad(v, 16)), combine(lane_quad(v, 32), lane_quad(v, 48)));
+  v = combine(combine(lane_quad(v, 0), lane_quad(v, 16)),
+              combine(lane_quad(v, 32), lane_quad(v, 48)));
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   if ((threadIdx.x & (kWave - 1)) == 0) lds[wave] = v;
   __syncthreads();

@@ -28,9 +28,14 @@
 //   slots (a ballot per step; the wave's count is uniform, so no atomics); then the prefix,
 //   held in registers (or re-read from L2 for unaligned or short rows), is compacted too.  For
 //   LLM logits that is a few hundred values (a few dozen per wave); kth and both sums come from
-//   LDS with no further pass over the row, each wave reading back its own segment.  If more
-//   than kSeg values qualify in one wave (flat or adversarial rows), an exact 4-pass radix
-//   select over the row and a summing pass take over.  Rows without a top-k sum over the whole row in a second pass.
+//   LDS with no further pass over the row, each wave reading back its own segment (into
+//   registers, one candidate per lane, when no wave holds more than 64).
+//   Tail: one exchange for the counts, flags and maximum; kth by an exact radix select over the
+//   candidates, four 8-bit rounds of one barrier each (every wave scans the histogram itself
+//   and finds the digit in scalar registers); the two FP64 sums; the verdict.
+//   Fallbacks: if more than kSeg values qualify in one wave (flat or adversarial rows), an
+//   exact 4-pass radix select over the row and a summing pass take over.  Rows without a top-k
+//   sum over the whole row in a second pass.
 
 #include <hip/hip_runtime.h>
 
@@ -124,9 +129,11 @@ __device__ __forceinline__ double read_lane(double v, int lane) {
   return __longlong_as_double(static_cast<long long>(lo | (hi << 32)));
 }
 
-// op over the wave's 64 lanes, the same value in every lane and a fixed order: a butterfly
-// inside each 16-lane row (quad_perm [1,0,3,2], [2,3,0,1], row_ror 4, row_ror 8), then the
-// four row results as (r0 op r1) op (r2 op r3).  Every lane must be active.
+// op over the wave's 64 lanes, returned in every lane, in a fixed order: inside each 16-lane
+// row, partners at quad_perm [1,0,3,2] and [2,3,0,1], then row_ror 4 and row_ror 8 (every
+// lane then holds its row's result; for a non-associative op the lanes may differ in how it
+// was grouped, and only lanes 0, 16, 32 and 48 are read), then (r0 op r1) op (r2 op r3).
+// Every lane must be active.
 template <typename T, typename Op>
 __device__ __forceinline__ T wave_reduce(T v, Op op) {
   v = op(v, dpp<0xB1>(v));
@@ -138,9 +145,11 @@ __device__ __forceinline__ T wave_reduce(T v, Op op) {
 
 // Workgroup sum of `count`, OR of `flag` and max of `v` (one barrier; the exchange slots are
 // not reused afterwards).  A lane's count and the wave's sum fit in 32 bits.
-__device__ void group_reduce(uint32_t lane_count, int64_t& count, int& flag, float& v, Scratch& s) {
+__device__ void group_reduce(uint32_t lane_count, int64_t& count, int& flag, float& v,
+                             Scratch& s) {
   const uint32_t c = wave_reduce(lane_count, [](uint32_t x, uint32_t y) { return x + y; });
-  const uint32_t f = wave_reduce(static_cast<uint32_t>(flag), [](uint32_t x, uint32_t y) { return x | y; });
+  const uint32_t f =
+      wave_reduce(static_cast<uint32_t>(flag), [](uint32_t x, uint32_t y) { return x | y; });
   const float mx = wave_reduce(v, [](float x, float y) { return fmaxf(x, y); });
   if (lane_id() == 0) {
     s.red_i[wave_id()] = c;
@@ -544,7 +553,8 @@ extern "C" int pck_check_members_ex(const PckMemberArgs* args, void* stream) {
       a.vocab > 0x7FFFFFFF || a.k_lim < 0 || a.k_lim > a.vocab)
     return hipErrorInvalidValue;
   if (a.rows == 0) return hipSuccess;
-  if (!a.logits || !a.tokens || (a.temperature && (!a.temperature_index || a.temperature_count < 1)))
+  if (!a.logits || !a.tokens ||
+      (a.temperature && (!a.temperature_index || a.temperature_count < 1)))
     return hipErrorInvalidValue;
   if (a.all_k && a.k_lim < 1) return hipErrorInvalidValue;
   pck::member_kernel<<<dim3(static_cast<unsigned>(a.rows)), dim3(pck::kThreads), 0,

@@ -98,7 +98,8 @@ __global__ void __launch_bounds__(kWave) mfma_bf16_k8_kernel(const uint16_t* a, 
 __global__ void __launch_bounds__(256) round_up_kernel(const double* a, const double* b,
                                                        double* out, int64_t n) {
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += stride) {
     out[4 * i] = pck::mul_up(a[i], b[i]);
     out[4 * i + 1] = pck::mul_up_pos(a[i], b[i]);
     out[4 * i + 2] = pck::add_up(a[i], b[i]);
