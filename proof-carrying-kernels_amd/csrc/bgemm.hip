@@ -279,7 +279,8 @@ __device__ __forceinline__ s16x4 x_step(const u32x4& v, int j) {
 struct PackedArgs {
   const char* Wp;  // packed weights, ceil(m / 32) tiles
   const char* Xp;  // packed activations, ceil(batch / 32) tiles
-  float* Y;        // (batch, m) FP32, row-major, m % 4 == 0, 16-byte aligned
+  float* Y;        // (batch, ldy) FP32, row-major, columns 0 .. m - 1 written, 16-byte aligned
+  int64_t ldy;     // Y's row stride (a multiple of 4)
   int64_t m;
   int64_t n;
   int64_t batch;
@@ -563,7 +564,7 @@ __global__ void __launch_bounds__(kThreads) bgemm_packed_kernel(PackedArgs a) {
 #pragma unroll
         for (int t = 0; t < T; ++t) {
           const int64_t b = (cur.t0 + t) * 32 + l;
-          float* yrow = a.Y + b * a.m + rt * kRows + 4 * h;
+          float* yrow = a.Y + b * a.ldy + rt * kRows + 4 * h;
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             const int k = (r * T + t) * 4 + q;
@@ -745,12 +746,54 @@ hipError_t launch_rt(const PackedArgs& a, bool fp8, hipStream_t stream) {
   return fp8 ? launch_rtf<R, T, true>(a, stream) : launch_rtf<R, T, false>(a, stream);
 }
 
-hipError_t launch_packed(const PackedArgs& a, PackedShape shape, bool fp8, hipStream_t stream) {
+hipError_t launch_one(const PackedArgs& a, PackedShape shape, bool fp8, hipStream_t stream) {
   if (shape.rows == 2) return shape.tiles == 2 ? launch_rt<2, 2>(a, fp8, stream) : hipErrorInvalidValue;
   if (shape.tiles == 4) return launch_rt<1, 4>(a, fp8, stream);
   if (shape.tiles == 2) return launch_rt<1, 2>(a, fp8, stream);
   if (shape.tiles == 1) return launch_rt<1, 1>(a, fp8, stream);
   return hipErrorInvalidValue;
+}
+
+template <int R, int T>
+hipError_t resident_rt(bool fp8, int64_t* out) {
+  return fp8 ? resident_groups<R, T, true>(out) : resident_groups<R, T, false>(out);
+}
+
+hipError_t resident_for(PackedShape shape, bool fp8, int64_t* out) {
+  if (shape.rows == 2) return resident_rt<2, 2>(fp8, out);
+  if (shape.tiles == 4) return resident_rt<1, 4>(fp8, out);
+  if (shape.tiles == 2) return resident_rt<1, 2>(fp8, out);
+  return resident_rt<1, 1>(fp8, out);
+}
+
+// A looping shape (one resident workgroup per CU) whose item count is not a multiple of the
+// grid leaves the last round to part of the CUs (gate/up at B = 128: 896 items, 3.5 per CU).
+// Then the whole rounds run with the shape over the leading row tiles, and the remaining row
+// tiles as (1, 2) items, which are half or a quarter the size, in a second launch (measured on
+// gate/up at B = 128: 99.5 against 101.2 us for BF16, 96.1 against 101.3 us for FP8).  Every
+// output keeps its bits: an output's sum does not depend on the item that computes it.
+hipError_t launch_packed(const PackedArgs& a, PackedShape shape, bool fp8, hipStream_t stream) {
+  int64_t resident = 0;
+  hipError_t err = resident_for(shape, fp8, &resident);
+  if (err != hipSuccess) return err;
+  const int64_t passes = (a.batch_tiles + shape.tiles - 1) / shape.tiles;
+  const int64_t items = (a.row_tiles + shape.rows - 1) / shape.rows * passes;
+  const bool loops = resident < items && resident % passes == 0 && g_shape_override.tiles == 0;
+  if (!loops || items % resident == 0 || shape.tiles < 2) return launch_one(a, shape, fp8, stream);
+  const int64_t lead_tiles = items / resident * resident / passes * shape.rows;
+  if (lead_tiles <= 0 || lead_tiles >= a.row_tiles) return launch_one(a, shape, fp8, stream);
+  PackedArgs lead = a;
+  lead.row_tiles = lead_tiles;
+  lead.m = lead_tiles * kRows;
+  err = launch_one(lead, shape, fp8, stream);
+  if (err != hipSuccess) return err;
+  PackedArgs rest = a;
+  const int64_t w_tile_bytes = (a.n / kStep) / 2 * 64 * (fp8 ? 8 : 16);
+  rest.Wp = a.Wp + lead_tiles * w_tile_bytes;
+  rest.Y = a.Y + lead.m;
+  rest.row_tiles = a.row_tiles - lead_tiles;
+  rest.m = a.m - lead.m;
+  return launch_one(rest, PackedShape{1, 2}, fp8, stream);
 }
 
 }  // namespace
@@ -826,8 +869,8 @@ extern "C" int pck_bgemm_packed(int weight_kind, const void* Wp, const void* Xp,
   const int64_t batch_tiles = (batch + 31) / 32;
   // One buffer resource covers one weight tile and one pass's batch tiles (32-bit offsets).
   if ((n / kStep) * 32 * 16 * 4 > 0x7FFFFFFFll) return hipErrorInvalidValue;
-  const PackedArgs a{static_cast<const char*>(Wp), static_cast<const char*>(Xp), Y, m, n, batch,
-                     row_tiles, batch_tiles, 1};
+  const PackedArgs a{static_cast<const char*>(Wp), static_cast<const char*>(Xp), Y, m, m, n,
+                     batch, row_tiles, batch_tiles, 1};
   return launch_packed(a, choose_shape(row_tiles, batch, weight_kind == 1), weight_kind == 1,
                        static_cast<hipStream_t>(stream));
 }

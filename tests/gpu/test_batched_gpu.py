@@ -158,6 +158,30 @@ def test_workgroups_looping_over_items_give_the_model_bits(shape: tuple[int, int
     assert _same_bits(got8[np.ix_(bs, rows)], emulate_batched(Qv[rows], X[bs]))
 
 
+@pytest.mark.parametrize("B", [128, 100])
+def test_uneven_item_counts_split_into_two_launches_keep_the_bits(B: int) -> None:
+    """896 row tiles at four batch tiles (gate/up's shape at B = 128) give 896 looping items
+    for 256 workgroups: the built-in shape runs the first 768 row tiles and (1, 2) items the
+    last 128, in a second launch writing the same output.  Every output equals the element
+    kernel's, and a sample on both sides of the split equals the model, BF16 and FP8."""
+    m, n = 28672, 512
+    rng = np.random.default_rng(B)
+    W = _family(rng, (m, n), "wide")
+    X = _family(rng, (B, n), "real_x")
+    codes = rng.integers(0, 256, (m, n), dtype=np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0  # no NaN codes
+    Qv = e4m3_values()[codes].astype(np.float32)
+    print(f"batched split m={m} n={n} B={B}", flush=True)
+    got = _run(W, X, packed=True)
+    got8 = _run_codes(codes, X, packed=True)
+    assert _same_bits(got, _run(W, X))
+    assert _same_bits(got8, _run_codes(codes, X, packed=False))
+    rows = np.concatenate([np.arange(32 * 767, 32 * 769), np.arange(m - 32, m)])
+    bs = np.unique(np.concatenate([np.arange(4), np.arange(B - 4, B)]))
+    assert _same_bits(got[np.ix_(bs, rows)], emulate_batched(W[rows], X[bs]))
+    assert _same_bits(got8[np.ix_(bs, rows)], emulate_batched(Qv[rows], X[bs]))
+
+
 @pytest.mark.parametrize(("m", "n", "B"), [(64, 64, 32), (32, 8, 64)])
 def test_batched_tiny_magnitudes_match_model(m: int, n: int, B: int) -> None:
     """Products in the FP32 subnormal range; the results stay normal here (exactness of a
