@@ -94,7 +94,7 @@ def test_batched_bits_match_model(m: int, n: int, B: int, fam: str) -> None:
 TILE_SHAPES = [(36, 384, 33), (64, 1152, 100), (32, 4096, 300), (100, 2048, 5)]
 
 
-@pytest.mark.parametrize("shape", [(1, 1), (1, 2), (1, 4), (2, 2)], ids=str)
+@pytest.mark.parametrize("shape", [(1, 1), (1, 2), (1, 4), (2, 2), (3, 1)], ids=str)
 @pytest.mark.parametrize(("m", "n", "B"), TILE_SHAPES)
 def test_every_tile_setting_gives_the_model_bits(shape: tuple[int, int], m: int, n: int, B: int) -> None:
     """Weight and batch tiles per workgroup change only speed: BF16 and FP8 weights, every
@@ -122,9 +122,10 @@ def test_every_tile_setting_gives_the_model_bits(shape: tuple[int, int], m: int,
 # during the current one's last pass: n = 512 at two tiles, n = 1024 at three), of a partial
 # pass (n = 384: the ring is refilled at each item's start), several batch passes with the
 # row groups a multiple of 8 (m = 9728: the passes of a row group are items 8 apart), and a
-# ragged last row group and batch pass.
+# ragged last row group and batch pass (m = 19252: 602 row tiles, the last group of two).
 LOOP_SHAPES = [((2, 2), 19200, 512, 33), ((2, 2), 19200, 384, 64), ((1, 2), 9600, 1024, 100),
-               ((1, 4), 9728, 512, 300), ((1, 1), 9612, 512, 70)]  # fmt: skip
+               ((1, 4), 9728, 512, 300), ((1, 1), 9612, 512, 70),
+               ((3, 1), 19252, 512, 100)]  # fmt: skip
 
 
 @pytest.mark.parametrize(("shape", "m", "n", "B"), LOOP_SHAPES, ids=str)
