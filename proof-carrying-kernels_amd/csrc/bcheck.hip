@@ -68,7 +68,7 @@ constexpr int kPairsWG = 2 * kTile;  // pairs per workgroup tile
 constexpr int kColsWG = 2 * kTile;   // batch columns per workgroup tile
 constexpr int kStep = 32;            // K columns per step: 8 FP64 + 1 BF16 MFMA per tile
 constexpr int kRing = 2;             // steps of loads in flight per lane
-constexpr int kTargetGroups = 512;   // about two workgroups per CU on MI355X
+constexpr int kTargetGroups = 256;   // one workgroup per CU on MI355X
 constexpr int kFinishLanes = 16;    // finish: lanes per block's outputs (a DPP row)
 constexpr int kFinishCols = 64;     // finish: batch columns per workgroup
 constexpr double kSumSlack = 1.0 + 0x1p-16;
@@ -541,6 +541,7 @@ int64_t make_plan(const PckBatchCheckDesc* descs, int count, Plan& plan) {
   if (count < 1 || count > PCK_MAX_BATCH || descs == nullptr) return -1;
   plan.count = count;
   int64_t tile_columns = 0;  // sum of pair tiles x column tiles x n
+  int64_t max_n = 0;
   for (int g = 0; g < count; ++g) {
     const PckBatchCheckDesc& d = descs[g];
     if (d.num_blocks < 1 || d.checks < 1 || d.block < 4 || d.block % 4 != 0 ||
@@ -559,12 +560,21 @@ int64_t make_plan(const PckBatchCheckDesc* descs, int count, Plan& plan) {
     const int64_t pairs = d.checks * d.num_blocks;
     plan.pair_tiles[g] = (pairs + kPairsWG - 1) / kPairsWG;
     tile_columns += plan.pair_tiles[g] * ((d.batch + kColsWG - 1) / kColsWG) * d.n;
+    max_n = d.n > max_n ? d.n : max_n;
   }
-  // Segment length: a multiple of (quarters x kRing steps) giving about kTargetGroups
-  // workgroups.
+  // Segment length: the shortest multiple of (quarters x kRing steps) that keeps the grid within
+  // kTargetGroups workgroups, so that every CU holds at most one and no CU waits for a second
+  // (longest rows when no length does).
   constexpr int64_t kQuantum = kWaves * kRing * kStep;
   int64_t seg = (tile_columns / kTargetGroups + kQuantum - 1) / kQuantum * kQuantum;
   seg = seg < kQuantum ? kQuantum : seg;
+  for (;; seg += kQuantum) {
+    int64_t groups = 0;
+    for (int g = 0; g < count; ++g)
+      groups += plan.pair_tiles[g] * ((descs[g].batch + kColsWG - 1) / kColsWG) *
+                ((descs[g].n + seg - 1) / seg);
+    if (groups <= kTargetGroups || seg >= max_n) break;
+  }
   plan.seg_len = seg;
   plan.start[0] = 0;
   plan.finish[0] = 0;

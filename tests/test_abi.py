@@ -159,12 +159,13 @@ def _workspace(descs: ctypes.Array) -> tuple[int, int]:
 
 
 def test_batch_check_plan_sizes_the_llama_layer() -> None:
-    """The Llama-3-8B layer at B = 256, b = 128, K = 1: 442,368 tile-columns over 512
-    workgroups gives 1024-column segments (4 for n = 4096, 14 for n = 14336), so the partials
-    hold 256 x (48 x 4 + 32 x 4 + 224 x 4 + 32 x 14) FP64 pairs: 6,815,744 bytes."""
+    """The Llama-3-8B layer at B = 256, b = 128, K = 1: the shortest segment (a multiple of 256
+    columns) that keeps the partial grid within 256 workgroups is 2048 columns, 2 for n = 4096
+    and 7 for n = 14336 (10 x 8 x 2 + 1 x 8 x 7 = 216 workgroups; 1792 would give 304), so the
+    partials hold 256 x (48 x 2 + 32 x 2 + 224 x 2 + 32 x 7) FP64 pairs: 3,407,872 bytes."""
     layer = [(4096, 128, 48, 1, 256), (4096, 128, 32, 1, 256), (4096, 128, 224, 1, 256),
              (14336, 128, 32, 1, 256)]  # fmt: skip
-    assert _workspace(_check_descs(layer)) == (0, 6_815_744)
+    assert _workspace(_check_descs(layer)) == (0, 3_407_872)
 
 
 def test_batch_check_plan_rejects_what_32_bit_offsets_cannot_address() -> None:

@@ -175,7 +175,8 @@ def fake_desc(m: int, n: int, B: int, checks: int) -> PckBatchCheckDesc:
 
 def test_oversized_or_invalid_plans_enqueue_nothing() -> None:
     limit = lib().pck_batch_check_static_bytes()
-    descs = (PckBatchCheckDesc * 2)(fake_desc(28672, 4096, 1024, 4), fake_desc(4096, 14336, 1024, 4))
+    # 8 checks at B = 1024: 32 MiB of partial sums
+    descs = (PckBatchCheckDesc * 2)(fake_desc(28672, 4096, 1024, 8), fake_desc(4096, 14336, 1024, 8))
     need = ctypes.c_int64(0)
     check(lib().pck_batch_check_workspace(descs, 2, ctypes.byref(need)), "plan")
     assert need.value > limit
