@@ -36,8 +36,9 @@ as one `[bench detail]` JSON line on stderr.  The contract line holds:
                  per-bit flip detection rates, caught shortcut outputs with every escape
   membership     the top-k / top-p membership check, 256 x 151,936 logits
   vllm_plugin    the plugin wrapper's cost per step at the same size, beside the check alone
-  batched        B = 128 and 256: products, checker overhead, caught faulty columns (with the
-                 largest |rho| / tau of any column that escaped), hipBLASLt's time
+  batched        B = 128 and 256: products, checker overhead (one checker call per layer, and
+                 one per two layers), caught faulty columns (with the largest |rho| / tau of
+                 any column that escaped), hipBLASLt's time
   roofline       the dominant kernel (the BF16 tree GEMV instance used by q/k/v, o, gate/up):
                  algorithmic bytes per launch / its mean launch duration, from HIP events on
                  the launch stream around a graph that replays those launches back to back
@@ -720,10 +721,11 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense BF16 matrix peak
 def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: int = 7) -> dict:
     """BASELINE config 4 read literally: a Llama-3-8B decode layer at batch B = 128 and 256 on
     the matrix cores (four packed launches: q/k/v, o, gate/up, down; BF16 and FP8 weights),
-    every column of every output checked by one batched checker launch per layer (b = 128,
-    K = 1, the batched product's tree height).  32-layer passes over ``copies`` layer copies
-    (more than the MALL holds) are captured in a HIP graph and replayed.  Reported per B and
-    weight type: ms per layer with and without the checker, TFLOP/s (2 B sum(m n) per layer),
+    every column of every output checked by one batched checker call per layer (b = 128,
+    K = 1, the batched product's tree height), or by one call per two layers (their eight
+    outputs).  32-layer passes over ``copies`` layer copies (more than the MALL holds) are
+    captured in a HIP graph and replayed.  Reported per B and weight type: ms per layer with
+    and without the checker, TFLOP/s (2 B sum(m n) per layer),
     hipBLASLt's time for the same products (torch.mm, not bit-reproducible) and a fault
     campaign per kind (BF16 outputs, exponent and sign flips, a dropped reduction tail, BF16
     partial sums, a BF16 accumulator): planted faults caught and false alarms."""
@@ -770,6 +772,19 @@ def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: in
         torch.cuda.current_stream().wait_stream(side)  # the pass ends after its last check
         return out
 
+    def pair_pass(ls, xs):  # type: ignore[no-untyped-def]
+        """Every output checked, two layers' eight outputs per checker call (after the second
+        layer's products): the same checks, each launch pair spread over twice the work."""
+        out, held = [], []
+        for i in range(depth):  # depth is even
+            layer = ls[i % copies]
+            ys = [gemm_batched(Wp, X) for (Wp, _), X in zip(layer, xs)]
+            held += [(ch, X, Y) for (_, ch), X, Y in zip(layer, xs, ys)]
+            if i % 2 == 1:
+                out.append(check_batched(held))
+                held = []
+        return out
+
     def capture_pass(fn):  # type: ignore[no-untyped-def]
         warm = torch.cuda.Stream()
         warm.wait_stream(torch.cuda.current_stream())
@@ -810,8 +825,9 @@ def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: in
             g_gemm = capture_pass(lambda: [run_layer(ls[i % copies], xs, False) for i in range(depth)])
             g_chk = capture_pass(lambda: [run_layer(ls[i % copies], xs, True) for i in range(depth)])
             g_side = capture_pass(lambda: side_pass(ls, xs, side))  # noqa: B023
-            ms_gemm, ms_chk, ms_side = time_passes([g_gemm, g_chk, g_side])
-            del g_gemm, g_chk, g_side
+            g_pair = capture_pass(lambda: pair_pass(ls, xs))  # noqa: B023
+            ms_gemm, ms_chk, ms_side, ms_pair = time_passes([g_gemm, g_chk, g_side, g_pair])
+            del g_gemm, g_chk, g_side, g_pair
             # fault campaign on copy 0: every (block, column) cell of every output, per kind
             # (reference fault set, harness/numerics_sim.py:58-64 and harness/campaign.py:8-13)
             rng = np.random.default_rng(B + fp8)
@@ -857,6 +873,7 @@ def batched_layer(batches=(128, 256), copies: int = 2, depth: int = 32, reps: in
                 "mfma_peak_frac": round(B * flops_per_row / (ms_gemm / 1e3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
                 "checker_overhead_pct": round(100 * (ms_chk / ms_gemm - 1), 2),
                 "checker_overhead_side_stream_pct": round(100 * (ms_side / ms_gemm - 1), 2),
+                "checker_overhead_two_layers_pct": round(100 * (ms_pair / ms_gemm - 1), 2),
                 "faulty_columns": planted,  # per kind and launch: every column has the fault
                 "faulty_columns_caught": caught,
                 "faults_by_kind": {
@@ -1219,6 +1236,7 @@ def main() -> None:
     if batched is not None:
         line["batched"] = {
             key: {w: {"products_ms": e[w]["gemm_only_ms"], "checker_overhead_pct": e[w]["checker_overhead_pct"],
+                      "checker_overhead_two_layers_pct": e[w]["checker_overhead_two_layers_pct"],
                       "mfma_peak_frac": e[w]["mfma_peak_frac"],
                       "faulty_columns_caught": f"{e[w]['faulty_columns_caught']}/{e[w]['faulty_columns']}",
                       "escaped_max_rho_over_tau": e[w]["escaped_columns_max_rho_over_tau"],
