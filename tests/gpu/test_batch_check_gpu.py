@@ -313,6 +313,38 @@ def test_honest_llama_layer_passes(B: int) -> None:
             assert bool((res.rho.abs() <= res.tau).all())
 
 
+def test_two_layers_in_one_call_give_the_verdicts_of_two_calls() -> None:
+    """The two-layer schedule: eight outputs (two Llama-3-8B layers, B = 128) in one call plan
+    a longer K segment than four do, which moves only the rounding of rho and tau.  Verdicts
+    equal those of one call per layer: every honest column passes, and columns with a flipped
+    exponent bit in some outputs (layer 2's o and down) fail in both."""
+    g = torch.Generator().manual_seed(2)
+    shapes = [(6144, 4096), (4096, 4096), (28672, 4096), (4096, 14336)]
+    B = 128
+    items = []
+    for layer in range(2):
+        for m, n in shapes:
+            W = (torch.randn(m, n, generator=g) * 0.02).to(torch.bfloat16).cuda()
+            X = torch.randn(B, n, generator=g).to(torch.bfloat16).cuda()
+            Y = gemm_batched(pack_batched_weights(W), X)
+            if layer == 1 and m == 4096:  # o and down: flip bit 30 of one output in 5 columns
+                cols = torch.tensor([0, 17, 64, 101, 127], device="cuda")
+                rows = torch.randint(0, m, (5,), generator=g).cuda()
+                Yi = Y.view(torch.int32)
+                Yi[cols, rows] ^= 1 << 30
+            checker = GpuBlockedChecker(W, 128, batched_height(n), generator=torch.Generator().manual_seed(m + layer))
+            items.append((checker, X, Y))
+    print("batch check two layers in one call B=128", flush=True)
+    together = check_batched(items)
+    apart = check_batched(items[:4]) + check_batched(items[4:])
+    for i, (one, two) in enumerate(zip(together, apart)):
+        assert torch.equal(one.passed, two.passed), i
+        ok = one.passed  # finite rho there; the flipped outputs can make rho infinite
+        assert bool(((one.rho - two.rho).abs() <= 1e-6 * one.tau)[ok].all()), i
+    failing = [int((~r.verdict).any(dim=0).sum()) for r in together]
+    assert failing == [0, 0, 0, 0, 0, 5, 0, 5]
+
+
 def test_validation_messages() -> None:
     _, _, Wt, Xt = problem(128, 256, 4, seed=11)
     checker = GpuBlockedChecker(Wt, 64, batched_height(256), generator=torch.Generator().manual_seed(11))
