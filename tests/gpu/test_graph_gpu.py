@@ -1,6 +1,7 @@
 """HIP-graph capture of the hot path: a decode layer (grouped GEMVs and the blocked checker,
-BF16 and FP8) captured once and replayed several times, with eager work and synchronisation
-between replays, reproduces the eager outputs bit for bit on every replay."""
+BF16 and FP8) and the batched path (packs, packed products, the batched checker) captured once
+and replayed several times, with eager work and synchronisation between replays, reproduce the
+eager outputs bit for bit on every replay."""
 
 from __future__ import annotations
 
@@ -59,3 +60,51 @@ def test_graph_replays_match_eager(fp8: bool) -> None:
         for a, b in zip(g_res, eager_res):
             assert torch.equal(a.passed, b.passed) and a.passed.all()
             assert torch.equal(a.rho, b.rho) and torch.equal(a.tau, b.tau)
+
+
+def test_batched_layer_graph_replays_match_eager() -> None:
+    """The batched path under capture: activation packs, packed products (gate/up at B = 128
+    takes two launches, its uneven last round split off) and one batched checker call, BF16
+    and FP8 weights; every replay equals the eager run bit for bit, with eager work between."""
+    from pck.cuda import batched_height, check_batched, gemm_batched, pack_batched_weights
+
+    gen = torch.Generator().manual_seed(12)
+    B = 128
+    items = []
+    for m, n, fp8 in ((28672, 4096, False), (4096, 14336, True)):
+        W = (torch.randn(m, n, generator=gen) * 0.02).to(torch.bfloat16).cuda()
+        if fp8:
+            W = quantize_fp8(W)[0]
+        ref = W.to(torch.bfloat16)
+        X = torch.randn(B, n, generator=gen).to(torch.bfloat16).cuda()
+        checker = GpuBlockedChecker(ref, 128, batched_height(n), generator=gen)
+        items.append((pack_batched_weights(W), X, checker))
+
+    def step():  # type: ignore[no-untyped-def]
+        ys = [gemm_batched(Wp, X) for Wp, X, _ in items]
+        return ys, check_batched([(c, X, Y) for (_, X, c), Y in zip(items, ys)])
+
+    print("batched layer under graph capture", flush=True)
+    eager_y, eager_res = step()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        g_y, g_res = step()
+    for replay in range(4):
+        for y in g_y:
+            y.fill_(float("nan"))  # eager work between replays; the replay must overwrite it
+        for r in g_res:
+            r.rho.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(g_y, eager_y):
+            assert torch.equal(a.view(torch.int32), b.view(torch.int32)), replay
+        for a, b in zip(g_res, eager_res):
+            assert torch.equal(a.passed, b.passed) and bool(a.passed.all()), replay
+            assert torch.equal(a.rho, b.rho) and torch.equal(a.tau, b.tau), replay
