@@ -1,7 +1,7 @@
 """HIP-graph capture of the hot path: a decode layer (grouped GEMVs and the blocked checker,
-BF16 and FP8) and the batched path (packs, packed products, the batched checker) captured once
-and replayed several times, with eager work and synchronisation between replays, reproduce the
-eager outputs bit for bit on every replay."""
+BF16 and FP8), the batched path (packs, packed products, the batched checker) and the
+membership check, each captured once and replayed several times with eager work and
+synchronisation between replays, reproduce the eager outputs bit for bit on every replay."""
 
 from __future__ import annotations
 
@@ -108,3 +108,48 @@ def test_batched_layer_graph_replays_match_eager() -> None:
         for a, b in zip(g_res, eager_res):
             assert torch.equal(a.passed, b.passed) and bool(a.passed.all()), replay
             assert torch.equal(a.rho, b.rho) and torch.equal(a.tau, b.tau), replay
+
+
+def test_membership_graph_replays_match_eager() -> None:
+    """The membership check under capture (B = 64, V = 151936, top-k and top-p rows, greedy
+    rows, one planted out-of-set token), given the host copy of top-k as vLLM passes it: every
+    replay equals the eager run, with eager work between replays."""
+    from pck.member import check_members
+
+    gen = torch.Generator().manual_seed(13)
+    B, V = 64, 151936
+    logits = (torch.randn(B, V, generator=gen) * 3).cuda()
+    top_k = torch.randint(1, 200, (B,), generator=gen).cuda()
+    top_p = (torch.rand(B, generator=gen) * 0.5 + 0.5).cuda()
+    greedy = torch.zeros(B, dtype=torch.bool)
+    greedy[::9] = True
+    greedy = greedy.cuda()
+    tokens = logits.argmax(dim=1)
+    tokens[5] = logits[5].argmin()  # outside every set: rejected
+
+    top_k_host = top_k.cpu().numpy()  # a capture cannot copy top-k to the host itself
+
+    def step():  # type: ignore[no-untyped-def]
+        return check_members(logits, tokens, top_k=top_k, top_p=top_p, greedy=greedy,
+                             top_k_host=top_k_host)  # fmt: skip
+
+    print("membership under graph capture", flush=True)
+    eager = step()
+    torch.cuda.synchronize()
+    assert not bool(eager["ok"][5]) and int(eager["ok"].sum()) == B - 1
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        got = step()
+    for replay in range(4):
+        for t in got.values():
+            t.zero_()  # eager work between replays; the replay must overwrite it
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for key in ("ok", "above", "mass_above"):
+            assert torch.equal(got[key], eager[key]), (key, replay)
