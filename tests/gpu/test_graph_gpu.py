@@ -1,7 +1,8 @@
 """HIP-graph capture of the hot path: a decode layer (grouped GEMVs and the blocked checker,
-BF16 and FP8), the batched path (packs, packed products, the batched checker) and the
-membership check, each captured once and replayed several times with eager work and
-synchronisation between replays, reproduce the eager outputs bit for bit on every replay."""
+BF16 and FP8), the batched path (packs, packed products, the batched checker), the membership
+check and the set-sampling checker, each captured once and replayed several times with eager
+work and synchronisation between replays, reproduce the eager outputs bit for bit on every
+replay."""
 
 from __future__ import annotations
 
@@ -153,3 +154,52 @@ def test_membership_graph_replays_match_eager() -> None:
         torch.cuda.synchronize()
         for key in ("ok", "above", "mass_above"):
             assert torch.equal(got[key], eager[key]), (key, replay)
+
+
+def test_set_sampling_checks_graph_replays_match_eager() -> None:
+    """The set-sampling checker under capture (top-k and top-p, B = 8, V = 151936, one row's
+    top-k set with a swapped member): every replay equals the eager run, with eager work
+    between replays."""
+    from pck.cuda import check_topk_gpu, check_topp_gpu, topk_sample, topp_select
+
+    gen = torch.Generator().manual_seed(14)
+    B, V, k, p = 8, 151936, 50, 0.9
+    logits = (torch.randn(B, V, generator=gen) * 2).cuda()
+    selected, _ = topk_sample(logits, k)
+    selected[3, 0] = logits[3].argmin()  # not a top-k set
+    nucleus, lengths = topp_select(logits, p)
+
+    def step():  # type: ignore[no-untyped-def]
+        return check_topk_gpu(logits, selected, k), check_topp_gpu(logits, nucleus, lengths, p)
+
+    print("set-sampling checks under graph capture", flush=True)
+    eager = step()
+    torch.cuda.synchronize()
+    assert not bool(eager[0].passed[3]) and int(eager[0].passed.sum()) == B - 1
+    assert bool(eager[1].passed.all())
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        got = step()
+    fields = ("passed", "min_selected", "max_rejected", "mass", "mass_without_smallest")
+    for replay in range(4):
+        for res in got:
+            for f in fields:
+                getattr(res, f).zero_()  # eager work between replays; the replay must overwrite it
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(got, eager):
+            for f in fields:
+                assert torch.equal(_bits(getattr(a, f)), _bits(getattr(b, f))), (f, replay)
+
+
+def _bits(t: torch.Tensor) -> torch.Tensor:
+    """The tensor's bit patterns (equal NaNs compare equal)."""
+    if t.dtype == torch.float64:
+        return t.view(torch.int64)
+    return t.view(torch.int32) if t.dtype == torch.float32 else t
