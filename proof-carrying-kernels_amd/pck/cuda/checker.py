@@ -484,13 +484,17 @@ def check_batched(
     Y (B, m) FP32 (``Y = X W^T``): every column of Y is checked as `check_many` checks one
     GEMV output, with the checker's bank, signs and constants (build the checker with the
     height of the batched product's tree).  Up to eight outputs per launch; results have
-    shape (checks, num_blocks, B), and ``verdict`` is then (num_blocks, B).  No reference
+    shape (checks, num_blocks, B) (B = 0 gives empty results and launches nothing), and
+    ``verdict`` is then (num_blocks, B).  No reference
     counterpart: the reference checks one vector per call (`src/pck/cuda/checker.py:143-171`).
     """
-    direct = [item for item in items if _batched_kernel_fits(*item)]
     out: dict[int, CheckResult] = {}
+    for item in items:  # an empty batch: validated, nothing to launch
+        if item[1].dim() == 2 and item[1].size(0) == 0:
+            out[id(item)] = _describe_batched([item])[1][0]
+    direct = [item for item in items if id(item) not in out and _batched_kernel_fits(*item)]
     for item in items:
-        if not _batched_kernel_fits(*item):
+        if id(item) not in out and not _batched_kernel_fits(*item):
             out[id(item)] = _check_columns(*item)
     for res, item in zip(_check_batched_direct(direct), direct):
         out[id(item)] = res
@@ -531,6 +535,17 @@ def batched_descriptors(
 ) -> tuple[Any, list[CheckResult], torch.device]:
     """Validated launch descriptors (a `PckBatchCheckDesc` array) for up to eight
     ``(checker, X, Y)`` items, freshly allocated results, and the device."""
+    descs, results, device = _describe_batched(chunk)
+    if any(X.size(0) == 0 for _, X, _ in chunk):
+        raise RuntimeError("batch size must be positive")
+    return descs, results, device
+
+
+def _describe_batched(
+    chunk: Sequence[tuple[GpuBlockedChecker, torch.Tensor, torch.Tensor]],
+) -> tuple[Any, list[CheckResult], torch.device]:
+    """`batched_descriptors` without the batch-size rule: an item with B = 0 gets results of
+    shape (checks, num_blocks, 0)."""
     descs = (PckBatchCheckDesc * len(chunk))()
     results: list[CheckResult] = []
     device = None
@@ -559,8 +574,6 @@ def batched_descriptors(
             ch.num_blocks, ch.checks, B, ch.coef, ch.geps, ch.tau_floor,
         )  # fmt: skip
     assert device is not None
-    if any(X.size(0) == 0 for _, X, _ in chunk):
-        raise RuntimeError("batch size must be positive")
     return descs, results, device
 
 

@@ -357,3 +357,13 @@ def test_validation_messages() -> None:
         checker.check_batched(Xt, Y[:3].contiguous())
     with pytest.raises(RuntimeError, match="CUDA"):
         checker.check_batched(Xt, Y.cpu())
+    # an empty batch is validated like any other and gives empty results, as gemm_batched
+    # gives an empty product
+    X0 = Xt[:0].contiguous()
+    Y0 = gemm_batched(Wt, X0)
+    res = checker.check_batched(X0, Y0)
+    assert res.passed.shape == (1, 2, 0) and res.rho.shape == res.tau.shape == (1, 2, 0)
+    with pytest.raises(RuntimeError, match="X must be"):
+        checker.check_batched(X0.float(), Y0)
+    with pytest.raises(RuntimeError, match="shape"):
+        checker.check_batched(X0, Y[:0, :64].contiguous())
