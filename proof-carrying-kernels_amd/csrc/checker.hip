@@ -30,12 +30,16 @@ __global__ void __launch_bounds__(check::kThreads) blocked_check_kernel(const Pc
   __shared__ check::Quad lds[check::kWaves];
   const int64_t item = blockIdx.x;
   const int g = check::owner(batch, item);
-  // Rows of more than 8 quads per lane keep 16 in flight (one round trip for n up to 16 K);
-  // the order, and so every bit, is the same for any number in flight.
-  if (batch.desc[g].n > 8 * 4 * check::kThreads)
+  // Quads in flight per lane: all of a row's up to 16 K columns in one round trip, without
+  // redundant loads for rows of at most 4 quads per lane; the order, and so every bit, is the
+  // same for any number in flight.
+  const int64_t n = batch.desc[g].n;
+  if (n > 8 * 4 * check::kThreads)
     check::check_pair<16>(batch, item, g, lds);
-  else
+  else if (n > 4 * 4 * check::kThreads)
     check::check_pair<8>(batch, item, g, lds);
+  else
+    check::check_pair<4>(batch, item, g, lds);
 }
 
 constexpr int kRowSumWaves = 4;
