@@ -30,12 +30,14 @@ __global__ void __launch_bounds__(check::kThreads) blocked_check_kernel(const Pc
   __shared__ check::Quad lds[check::kWaves];
   const int64_t item = blockIdx.x;
   const int g = check::owner(batch, item);
-  // Quads in flight per lane: all of a row's up to 16 K columns in one round trip, without
-  // redundant loads for rows of at most 4 quads per lane; the order, and so every bit, is the
-  // same for any number in flight.
+  // Quads in flight per lane: all of a row's up to 16 K columns in one round trip, and no more
+  // than the row has per lane up to 14 quads (a longer ring only re-loads quad 0); the order,
+  // and so every bit, is the same for any number in flight.
   const int64_t n = batch.desc[g].n;
-  if (n > 8 * 4 * check::kThreads)
+  if (n > 14 * 4 * check::kThreads)
     check::check_pair<16>(batch, item, g, lds);
+  else if (n > 8 * 4 * check::kThreads)
+    check::check_pair<14>(batch, item, g, lds);
   else if (n > 4 * 4 * check::kThreads)
     check::check_pair<8>(batch, item, g, lds);
   else
