@@ -354,8 +354,9 @@ __device__ __forceinline__ double row_sum(double v) {
 //   the float4 groups q, q + 16, ... (rows 64 i + 4 q .. + 3) of the block in each of them, all
 //   loads of a pass in flight (the block's signs once for the four columns); DPP row sums.
 //   Partials: lane t takes column t % 64 and segments t / 64, t / 64 + 4, ... in order (one load
-//   instruction reads 64 consecutive columns of one segment); the four subsets meet in LDS as
-//   (p0 + p1) + (p2 + p3).
+//   instruction reads 64 consecutive columns of one segment), four of them in flight per pass
+//   (a layer's plan gives a subset 1-4 segments; more in flight would re-read the last one);
+//   the four subsets meet in LDS as (p0 + p1) + (p2 + p3).
 //   Lanes 0 .. 63 then form rho, tau and the verdict of one column each; every operand of tau is
 //   non-negative (the plan checks the constants), so the branch-free round-up operations apply.
 __global__ void __launch_bounds__(kThreads) finish_kernel(const Plan plan) {
@@ -413,7 +414,7 @@ __global__ void __launch_bounds__(kThreads) finish_kernel(const Plan plan) {
   const int sub = __builtin_amdgcn_readfirstlane(t / kFinishCols);  // and its segment subset
   const uint32_t p_off = static_cast<uint32_t>((pc < cols ? pc : cols - 1) * 8);
   const uint32_t seg_bytes = static_cast<uint32_t>(f.outs * 8);  // one segment's partials
-  constexpr int kAhead = 8;
+  constexpr int kAhead = 4;
   int k = 0;
   do {  // checks >= 1 (the plan rejects fewer)
     const int64_t pair = static_cast<int64_t>(k) * nb + beta;
