@@ -361,17 +361,24 @@ __global__ void __launch_bounds__(kGroupThreads) gemv_tree_kernel(const GemvBatc
 
 // A GEMV launch that also checks outputs of earlier launches: the first workgroups of the grid
 // each run one (check, block) pair of `ride` (the standalone checker's code, so rho, tau and the
-// verdicts are bit-identical to pck_blocked_check), the rest compute the GEMV rows.  The checked y were written by launches that finished before this one
-// started (stream order), and the checker workgroups are separate wavefronts that read them from
-// memory; their latency hides behind the GEMV's streaming, and the bank reads add about 2.3%
-// (BF16, b = 128) to the bytes.
+// verdicts are bit-identical to pck_blocked_check), the rest compute the GEMV rows.  The checked
+// y were written by launches that finished before this one started (stream order), and the
+// checker workgroups are separate wavefronts that read them from memory; their latency hides
+// behind the GEMV's streaming, and the bank reads add about 2.3% (BF16, b = 128) to the bytes.
+// Rows longer than 4,096 columns keep 8 quads per lane in flight (a 14,336-column row in two
+// round trips instead of four); more would push the kernel past 128 VGPRs and halve the GEMV
+// waves a SIMD holds.
 template <int T, int R, int U, bool kFp8, bool kPad, bool kNt>
 __global__ void __launch_bounds__(kGroupThreads)
     gemv_ride_kernel(const GemvBatch batch, const PckCheckBatch ride) {
   __shared__ check::Quad lds[check::kWaves];
   const int64_t items = ride.start[ride.count];
   if (static_cast<int64_t>(blockIdx.x) < items) {
-    check::check_pair<4>(ride, blockIdx.x, check::owner(ride, blockIdx.x), lds);
+    const int g = check::owner(ride, blockIdx.x);
+    if (ride.desc[g].n > 4 * 4 * check::kThreads)
+      check::check_pair<8>(ride, blockIdx.x, g, lds);
+    else
+      check::check_pair<4>(ride, blockIdx.x, g, lds);
     return;
   }
   gemv_rows<T, R, U, kFp8, true, kPad, kNt>(batch, static_cast<int64_t>(blockIdx.x) - items);
