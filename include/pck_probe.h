@@ -46,6 +46,13 @@ int pck_probe_mfma_bf16_k8(const uint16_t* a, const uint16_t* b, const float* c,
  * general forms' bits. */
 int pck_probe_round_up(const double* a, const double* b, double* out, int64_t n, void* stream);
 
+/* The checkers' in-hardware upward sums (csrc/rounding.h add_up_rm2 / add_up_rm4, one add each
+ * under the wave's round-toward-+inf mode) for n pairs: out[3 i] and out[3 i + 1] = RU(a[i] +
+ * b[i]) from each form; out[3 i + 2] = an ordinary add issued after them, RN(a[i] + b[i]) when
+ * the forms leave the rounding mode as they found it. */
+int pck_probe_round_up_mode(const double* a, const double* b, double* out, int64_t n,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,8 +17,9 @@
 // FP64 operation, so rho's rounding error is at most gamma_H(u64) (sum |c_j x_j| + sum |y_i|)
 // for the depth H <= n + b + 1 of its evaluation, which the host's geps (reference formula,
 // which also carries the reference's FP32 Dot2 term) covers.  s and the sums of |y| add exact
-// non-negative terms (a_j |x_j| has 16 significand bits) with error-free round-up additions in
-// FP64.  The reference adds the same terms in FP32, rounding up, and then in FP64; since every
+// non-negative terms (a_j |x_j| has 16 significand bits) with upward-rounded FP64 additions:
+// in the bank loop and the workgroup reduction one add each under the wave's upward rounding
+// mode (add_up_rm4 / add_up_rm2), elsewhere the TwoSum form add_up_nonneg, the same bits.  The reference adds the same terms in FP32, rounding up, and then in FP64; since every
 // FP32 partial it forms is at least the exact sum, and the FP64 sums here are exact whenever
 // its FP32 ones are, this s is at most the reference's (equal on typical inputs), and so is
 // tau.  An s beyond the FP32 range becomes +inf (tau = inf, a failed block), as the
@@ -82,7 +83,9 @@ struct Quad {
 };
 
 __device__ __forceinline__ Quad combine(const Quad& a, const Quad& b) {
-  return Quad{a.cx + b.cx, add_up_nonneg(a.s, b.s), a.ry + b.ry, add_up_nonneg(a.yabs, b.yabs)};
+  double s = a.s, yabs = a.yabs;
+  add_up_rm2(s, b.s, yabs, b.yabs);  // RU, as add_up_nonneg
+  return Quad{a.cx + b.cx, s, a.ry + b.ry, yabs};
 }
 
 // v in the lane that DPP pattern kCtrl names (every lane has a source for the patterns used).
@@ -230,10 +233,15 @@ __device__ __forceinline__ void check_pair(const PckCheckBatch& batch, int64_t i
                                      __uint_as_float(__float_as_uint(cv[k].z) & keep),
                                      __uint_as_float(__float_as_uint(cv[k].w) & keep));
         const uint2 xx = make_uint2(xv[k].x & keep, xv[k].y & keep);
-        column(cx[0], sa[0], c.x, bf16_lo(av[k].x), bf16_lo(xx.x));
-        column(cx[1], sa[1], c.y, bf16_hi(av[k].x), bf16_hi(xx.x));
-        column(cx[2], sa[2], c.z, bf16_lo(av[k].y), bf16_lo(xx.y));
-        column(cx[3], sa[3], c.w, bf16_hi(av[k].y), bf16_hi(xx.y));
+        const double x0 = bf16_lo(xx.x), x1 = bf16_hi(xx.x), x2 = bf16_lo(xx.y),
+                     x3 = bf16_hi(xx.y);
+        cx[0] = __builtin_fma(static_cast<double>(c.x), x0, cx[0]);
+        cx[1] = __builtin_fma(static_cast<double>(c.y), x1, cx[1]);
+        cx[2] = __builtin_fma(static_cast<double>(c.z), x2, cx[2]);
+        cx[3] = __builtin_fma(static_cast<double>(c.w), x3, cx[3]);
+        // a_j |x_j| is exact (16 significand bits); the four sums round upward in hardware
+        add_up_rm4(sa, bf16_lo(av[k].x) * __builtin_fabs(x0), bf16_hi(av[k].x) * __builtin_fabs(x1),
+                   bf16_lo(av[k].y) * __builtin_fabs(x2), bf16_hi(av[k].y) * __builtin_fabs(x3));
       }
     }
     done = nq * 4;

@@ -10,6 +10,8 @@
 //                             group of 8 K-slots split over the two lane halves, 4 per lane);
 //   pck_probe_mfma_bf16_16x16 v_mfma_f32_16x16x32_bf16 chains (the batched checker's a . |x|);
 //   pck_probe_round_up        rounding.h's upward products and sums, general and branch-free.
+//   pck_probe_round_up_mode   rounding.h's upward sums under the wave's rounding mode, and an
+//                             add the compiler places after them (round to nearest again).
 //
 // Operands are passed in lane order, so the probes embed no matrix layout: tile t, step s,
 // lane l reads its A and B operands at [(t * steps + s) * 64 + l] (8 or 4 BF16 values or one
@@ -107,6 +109,24 @@ __global__ void __launch_bounds__(256) round_up_kernel(const double* a, const do
   }
 }
 
+// out[3 i] = add_up_rm2's and out[3 i + 1] = add_up_rm4's RU(a + b) (one slot of each, the
+// others busy with other sums); out[3 i + 2] = (a + 0, rounded upward) + b as the compiler
+// issues it after the blocks, which must be the round-to-nearest a + b (the mode restored).
+__global__ void __launch_bounds__(256) round_up_mode_kernel(const double* a, const double* b,
+                                                            double* out, int64_t n) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += stride) {
+    double s0 = a[i], s1 = a[i];
+    pck::add_up_rm2(s0, b[i], s1, 0.0);
+    double q[4] = {1.0, 0x1p-60, a[i], 3.0};
+    pck::add_up_rm4(q, 0x1p-60, 1.0, b[i], 0x1p-70);
+    out[3 * i] = s0;
+    out[3 * i + 1] = q[2];
+    out[3 * i + 2] = s1 + b[i];
+  }
+}
+
 bool tiles_ok(int64_t tiles, int steps) {
   return tiles >= 1 && tiles <= (1 << 20) && steps >= 1 && steps <= 64;
 }
@@ -162,5 +182,16 @@ extern "C" int pck_probe_round_up(const double* a, const double* b, double* out,
   const int64_t blocks = (n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096;
   round_up_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                     static_cast<hipStream_t>(stream)>>>(a, b, out, n);
+  return hipGetLastError();
+}
+
+extern "C" int pck_probe_round_up_mode(const double* a, const double* b, double* out, int64_t n,
+                                       void* stream) {
+  if (n < 0 || (n > 0 && (a == nullptr || b == nullptr || out == nullptr)))
+    return hipErrorInvalidValue;
+  if (n == 0) return hipSuccess;
+  const int64_t blocks = (n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096;
+  round_up_mode_kernel<<<dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                         static_cast<hipStream_t>(stream)>>>(a, b, out, n);
   return hipGetLastError();
 }

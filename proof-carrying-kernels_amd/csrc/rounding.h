@@ -1,7 +1,8 @@
 // Directed rounding by error-free transformations, for gfx950 device code.
 //
 // AMDGCN has no per-instruction rounding mode, so the checkers' "round upward" operations are
-// built from round-to-nearest ones:
+// built from round-to-nearest ones (the hot upward sums of non-negative terms instead switch
+// the wave's rounding mode around their adds: add_up_rm2 / add_up_rm4 below):
 //   add_up(a, b): s = RN(a + b) and its exact error e = (a + b) - s by Knuth's TwoSum (exact
 //                 whenever s is finite); RU(a + b) = next_up(s) if e > 0, else s.
 //   mul_up(a, b): p = RN(a b) and its error e = fma(a, b, -p), exact unless a b is near the
@@ -70,6 +71,42 @@ __device__ __forceinline__ double add_up_nonneg(double a, double b) {
   const double err = (a - (s - bv)) + (b - bv);
   const double raised = __longlong_as_double(__double_as_longlong(s) + 1);
   return err > 0.0 ? raised : s;
+}
+
+// In-hardware upward additions for the checkers' inner loops and reductions: every a_i becomes
+// RU(a_i + b_i), one v_add_f64 each, issued while the wave's FP64 rounding mode (MODE bits 3:2,
+// which FP16 shares) is round toward +inf.  The mode write, the adds and the write that sets
+// the mode back to round to nearest even (the kernel's mode) form one asm block, so no
+// instruction the compiler schedules runs under the upward mode; each mode write is followed
+// by two wait states (s_nop 1) before anything that may depend on it.  The result is the
+// correctly rounded upward sum for any operands (NaN propagates as in any add), so for
+// a, b >= 0 it has add_up_nonneg's bits.  It replaces a TwoSum of seven dependent operations
+// by one add.
+__device__ __forceinline__ void add_up_rm2(double& a0, double b0, double& a1, double b1) {
+  __asm__ volatile(
+      "s_setreg_imm32_b32 hwreg(HW_REG_MODE, 2, 2), 1\n\t"
+      "s_nop 1\n\t"
+      "v_add_f64 %0, %0, %2\n\t"
+      "v_add_f64 %1, %1, %3\n\t"
+      "s_setreg_imm32_b32 hwreg(HW_REG_MODE, 2, 2), 0\n\t"
+      "s_nop 1"
+      : "+v"(a0), "+v"(a1)
+      : "v"(b0), "v"(b1));
+}
+
+__device__ __forceinline__ void add_up_rm4(double (&a)[4], double b0, double b1, double b2,
+                                           double b3) {
+  __asm__ volatile(
+      "s_setreg_imm32_b32 hwreg(HW_REG_MODE, 2, 2), 1\n\t"
+      "s_nop 1\n\t"
+      "v_add_f64 %0, %0, %4\n\t"
+      "v_add_f64 %1, %1, %5\n\t"
+      "v_add_f64 %2, %2, %6\n\t"
+      "v_add_f64 %3, %3, %7\n\t"
+      "s_setreg_imm32_b32 hwreg(HW_REG_MODE, 2, 2), 0\n\t"
+      "s_nop 1"
+      : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3])
+      : "v"(b0), "v"(b1), "v"(b2), "v"(b3));
 }
 
 // mul_up(a, b) for a, b >= +0 without branches, with the same result there: a zero factor

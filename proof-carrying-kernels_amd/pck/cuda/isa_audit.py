@@ -21,7 +21,11 @@ library's own flags (`pck._build`) to assembly and reports:
 - `v_rcp_f32` other than in the integer-division idiom (the first instruction that reads its
   result multiplies it by 0x5f7ffffc) or inside an IEEE division sequence (a
   `v_div_fixup_f32` within the next 40 vector instructions), and `v_rcp_f64` other than inside
-  an IEEE division sequence (a `v_div_fixup_f64` within the next 40 vector instructions).
+  an IEEE division sequence (a `v_div_fixup_f64` within the next 40 vector instructions);
+- any write of a hardware register (`s_setreg*`, `s_round_mode`, `s_denorm_mode`) other than
+  the checkers' upward-add window: the FP64 rounding field set to round toward +inf, then
+  only `v_add_f64` and `s_nop`, then the field set back to round to nearest even (an
+  unclosed window, or any other instruction inside one, is reported).
 
 The library's other sources (the agent's templates, their INT8 copy, the read stream) are held
 to the same rules: the templates are bit-exact FP32 trees like the trusted GEMV.
@@ -60,6 +64,10 @@ FP32_MULADD = re.compile(r"^v_(fma|fmac|mad|mac|fmamk|fmaak|madmk|madak)_f32|^v_
 INT_DIV_FMAMK = re.compile(r"^v_fmamk_f32\b.*,\s*0x(4f800000|cf800000)\s*,")
 TRANSCENDENTAL = re.compile(r"^v_(exp|log)_f32|^v_(rsq|sqrt)_f(16|32|64)")
 INT_DIV_MUL = re.compile(r"^v_mul_f32\w*\s.*0x5f7ffffc")
+MODE_WRITE = re.compile(r"^s_(setreg\w*|round_mode|denorm_mode)$")
+UPWARD_ON = "s_setreg_imm32_b32 hwreg(HW_REG_MODE, 2, 2), 1"
+UPWARD_OFF = "s_setreg_imm32_b32 hwreg(HW_REG_MODE, 2, 2), 0"
+UPWARD_BODY = re.compile(r"^(s_nop|v_add_f64)$")
 
 _INSN = re.compile(r"^\s+([a-z][a-z0-9_]*)(?:\s+(.*))?$")
 _KERNEL = re.compile(r"^\s*\.amdhsa_kernel\s+(\S+)")
@@ -125,8 +133,17 @@ def violations(source: str, asm: str) -> list[str]:
                 return insns[j]
         return ""
 
+    upward = False  # inside an upward-add window
     for i, ins in enumerate(insns):
         op = ins.split(" ", 1)[0]
+        if ins == UPWARD_ON and not upward:
+            upward = True
+        elif ins == UPWARD_OFF and upward:
+            upward = False
+        elif MODE_WRITE.match(op):
+            found.append(f"{source}: hardware-register write outside the upward-add window: {ins}")
+        elif upward and not UPWARD_BODY.match(op):
+            found.append(f"{source}: instruction under the upward rounding mode: {ins}")
         if PACKED_FP32.match(op):
             found.append(f"{source}: packed FP32 instruction: {ins}")
         if SCALAR_WRITE.match(op):
@@ -143,6 +160,8 @@ def violations(source: str, asm: str) -> list[str]:
         if op.startswith("v_rcp_f64"):
             if not any(w.startswith("v_div_fixup_f64") for w in vector_window(i, 40)):
                 found.append(f"{source}: v_rcp_f64 outside an IEEE division sequence: {ins}")
+    if upward:
+        found.append(f"{source}: upward rounding mode left set at the end of the code")
     modes = kernel_modes(asm)
     if not modes:
         found.append(f"{source}: no kernel descriptors found")

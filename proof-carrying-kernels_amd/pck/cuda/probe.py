@@ -28,6 +28,7 @@ SIGNATURES = {
     "pck_probe_mfma_bf16_16x16": [_p, _p, _p, _p, _i64, _int, _p],
     "pck_probe_mfma_bf16_k8": [_p, _p, _p, _p, _i64, _int, _p],
     "pck_probe_round_up": [_p, _p, _p, _i64, _p],
+    "pck_probe_round_up_mode": [_p, _p, _p, _i64, _p],
 }
 _handle: ctypes.CDLL | None = None
 
@@ -73,6 +74,18 @@ def round_up(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     with torch.cuda.device(a.device):
         check(lib().pck_probe_round_up(a.data_ptr(), b.data_ptr(), out.data_ptr(), a.numel(),
                                        stream_handle(a.device)), "round_up probe")  # fmt: skip
+    return out
+
+
+def round_up_mode(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """(n, 3) FP64: the device's add_up_rm2 and add_up_rm4 sums of the FP64 CUDA tensors ``a``
+    and ``b`` (same shape, flattened), and an ordinary add issued after them."""
+    a = _cuda(a, torch.float64, tuple(a.shape), "a")
+    b = _cuda(b, torch.float64, tuple(a.shape), "b")
+    out = torch.empty((a.numel(), 3), dtype=torch.float64, device=a.device)
+    with torch.cuda.device(a.device):
+        check(lib().pck_probe_round_up_mode(a.data_ptr(), b.data_ptr(), out.data_ptr(), a.numel(),
+                                            stream_handle(a.device)), "round_up_mode probe")  # fmt: skip
     return out
 
 

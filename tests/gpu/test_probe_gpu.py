@@ -288,3 +288,33 @@ def test_general_round_up_forms_on_negative_operands() -> None:
         for got, exact, rn in ((mul, Fraction(x) * Fraction(y), x * y), (add, Fraction(x) + Fraction(y), x + y)):
             ru = rn if Fraction(rn) >= exact else np.nextafter(rn, np.inf)
             assert got == ru, (x, y, got, ru)
+
+
+def test_round_up_under_the_wave_rounding_mode() -> None:
+    """add_up_rm2 / add_up_rm4 (one add under the upward mode) give the TwoSum forms' bits, the
+    exact upward sum, and leave the mode at round to nearest for the adds after them."""
+    v = _special_nonneg()
+    a, b = (g.ravel() for g in np.meshgrid(v, v, indexing="ij"))
+    rng = np.random.default_rng(9)
+    ra = np.ldexp(rng.random(4096), rng.integers(-1100, 1000, 4096))
+    rb = np.ldexp(rng.random(4096), rng.integers(-1100, 1000, 4096))
+    na = np.ldexp(rng.random(2048) - 0.5, rng.integers(-200, 200, 2048))
+    nb = np.ldexp(rng.random(2048) - 0.5, rng.integers(-200, 200, 2048))
+    a, b = np.concatenate([a, ra, na]), np.concatenate([b, rb, nb])
+    ta, tb = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+    mode = probe.round_up_mode(ta, tb).cpu().numpy()
+    twosum = probe.round_up(ta, tb).cpu().numpy()
+    print("round-up-mode probe pairs", a.size, flush=True)
+    for col in (0, 1):
+        assert _same_bits(mode[:, col], twosum[:, 2]).all(), np.argwhere(~_same_bits(mode[:, col], twosum[:, 2]))[:4]
+    nonneg = (a >= 0) & (b >= 0)
+    assert _same_bits(mode[nonneg, 0], twosum[nonneg, 3]).all()
+    with np.errstate(over="ignore", invalid="ignore"):
+        rn = a + b
+    assert _same_bits(mode[:, 2], rn).all(), np.argwhere(~_same_bits(mode[:, 2], rn))[:4]
+    for x, y, got in zip(a, b, mode[:, 0]):
+        if not (np.isfinite(x) and np.isfinite(y)) or not np.isfinite(x + y):
+            continue
+        exact = Fraction(x) + Fraction(y)
+        ru = x + y if Fraction(x + y) >= exact else np.nextafter(x + y, np.inf)
+        assert got == ru, (x, y, got, ru)

@@ -75,6 +75,18 @@ def test_reciprocals_only_in_their_idioms() -> None:
     assert any("multiply-add" in v for v in audit.violations("template.hip", ieee_div32))
 
 
+def test_rounding_mode_writes_only_in_the_upward_add_window() -> None:
+    on, off = audit.UPWARD_ON, audit.UPWARD_OFF
+    window = f"\t{on}\n\ts_nop 1\n\tv_add_f64 v[2:3], v[2:3], v[4:5]\n\t{off}\n\ts_nop 1"
+    assert audit.violations("checker.hip", kernel(window)) == []
+    inside = f"\t{on}\n\tv_fma_f64 v[2:3], v[2:3], v[4:5], v[6:7]\n\t{off}"
+    assert any("under the upward" in v for v in audit.violations("checker.hip", kernel(inside)))
+    assert any("left set" in v for v in audit.violations("gemv.hip", kernel(f"\t{on}\n\tv_add_f64 v[2:3], v[2:3], v[4:5]")))
+    for other in ("s_setreg_b32 hwreg(HW_REG_MODE, 0, 4), s2", "s_setreg_imm32_b32 hwreg(HW_REG_MODE, 4, 4), 0",
+                  "s_round_mode 0x1", "s_denorm_mode 0x0", off):  # fmt: skip
+        assert any("hardware-register" in v for v in audit.violations("bcheck.hip", kernel(f"\t{other}")))
+
+
 def test_build_flags() -> None:
     assert audit.check_flags(_build.HIPCC_FLAGS) == []
     assert audit.check_flags([*_build.HIPCC_FLAGS, "-ffast-math"]) == ["forbidden flag -ffast-math"]
