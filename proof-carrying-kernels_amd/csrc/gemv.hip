@@ -501,15 +501,13 @@ TreeShape g_shape_override = {0, 0, 0};
 // Defaults from sweeps of every shape over each Llama-3-8B decode launch on MI355X.  BF16:
 // non-temporal weight loads won everywhere.  FP8 rows are half as long, so two rows per wave
 // keep as many bytes in flight as one BF16 row, except for a launch of at most 4096 rows (o),
-// where one row per wave and two positions ahead give twice the waves (4.9 against 5.4 us);
-// FP8 rows of more than two positions per lane (down) stream faster with plain loads
-// (12.5 against 13.0 us).
+// where one row per wave and two positions ahead give twice the waves (4.9 against 5.4 us).
+// The sweeps replay each launch over weight copies that do not fit the Infinity Cache (with
+// four copies of FP8 down, 235 MB, plain loads won from the cache; streamed from HBM, as in a
+// decode pass, non-temporal loads take 13.1 against 14.6 us).
 TreeShape choose_shape(int64_t per_lane, int64_t rows, bool fp8) {
   if (g_shape_override.rows > 0) return g_shape_override;
-  if (fp8) {
-    if (per_lane > 2) return TreeShape{2, 1, 0};
-    return rows <= 4096 ? TreeShape{1, 2, 1} : TreeShape{2, 1, 1};
-  }
+  if (fp8) return per_lane <= 2 && rows <= 4096 ? TreeShape{1, 2, 1} : TreeShape{2, 1, 1};
   return per_lane > 2 ? TreeShape{2, 2, 1} : TreeShape{1, 2, 1};
 }
 
@@ -598,10 +596,7 @@ template <bool kFp8>
 hipError_t launch_ride(GemvBatch& batch, bool pad, int64_t per_lane, const PckCheckBatch& ride,
                        hipStream_t stream) {
   if constexpr (kFp8) {
-    if (per_lane > 2) {
-      return pad ? launch_ride_shape<2, 1, true, true, false>(batch, ride, stream)
-                 : launch_ride_shape<2, 1, true, false, false>(batch, ride, stream);
-    }
+    (void)per_lane;
     return pad ? launch_ride_shape<2, 1, true, true>(batch, ride, stream)
                : launch_ride_shape<2, 1, true, false>(batch, ride, stream);
   } else {
