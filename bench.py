@@ -15,6 +15,9 @@ are replayed in alternating rounds, max(7, steps / 32) rounds whatever --steps i
   carried (b = 128, 256)  every output checked by the bank checker inside the next layer's
                      gate/up launch (pck_gemv_group_check, bit-identical to a standalone check);
                      the pass ends with one standalone check of the last gate, up and down
+  carried_check_many (b = 128)  the reference's call pattern (GEMVs, then check_many of the
+                     layer's outputs) through pck.cuda.CarriedChecker, which carries each
+                     layer's checks in the next gate/up launch
   inpass (b = 128, 256)   the GEMVs also write per-row checksums in the same pass
                      (pck_gemv_group_rowsums) and the row-sum checks ride as above
   serial, side_stream     one standalone check per layer, inline or on a second stream
@@ -174,11 +177,14 @@ def run_step(layer, with_check: bool, events=None):  # type: ignore[no-untyped-d
 # Modes of the batch-1 pass.  gemv: the GEMVs alone.  serial / side_stream: one standalone
 # bank-checker launch per layer after its GEMVs, on the same stream / on a side stream
 # overlapping the next layer (the reference's modes).  carried: the bank checks ride in later
-# GEMV launches.  inpass: the GEMVs compute their row sums in the same pass and the row-sum
-# checks ride in later launches (no bank read).  inpass_sums: the in-pass GEMVs with no checks
-# (the cost of the sums alone).  A _b256 suffix: checker block b = 256 instead of 128.
-MODES = ("gemv", "serial", "side_stream", "carried", "carried_b256", "inpass", "inpass_b256",
-         "inpass_sums")  # fmt: skip
+# GEMV launches.  carried_api: the reference's call pattern (the layer's GEMVs, then
+# check_many of its seven outputs) through pck.cuda.CarriedChecker, which carries each layer's
+# checks in the next gate/up launch and flushes the last layer's at the end.  inpass: the GEMVs
+# compute their row sums in the same pass and the row-sum checks ride in later launches (no
+# bank read).  inpass_sums: the in-pass GEMVs with no checks (the cost of the sums alone).  A
+# _b256 suffix: checker block b = 256 instead of 128.
+MODES = ("gemv", "serial", "side_stream", "carried", "carried_api", "carried_b256", "inpass",
+         "inpass_b256", "inpass_sums")  # fmt: skip
 # FP8 only, with the row scales applied (y = s z).  gemv_scale_after: the GEMVs, then one
 # elementwise multiply per output (the reference's order).  gemv_scaled: the GEMVs with the
 # multiply in their epilogue (pck_gemv_group_fp8_scaled).  carried_scaled: the carried checks
@@ -255,9 +261,21 @@ def capture(layers, mode: str, depth: int):  # type: ignore[no-untyped-def]
     gemv_scale_after torch's elementwise multiply (no memset, no library reduction).  Returns (graph, the pass's check results and outputs)."""
     import torch
 
-    from pck.cuda import check_many, gemv_group, gemv_group_fp8_scaled
+    from pck.cuda import CarriedChecker, check_many, gemv_group, gemv_group_fp8_scaled
 
     def body():  # type: ignore[no-untyped-def]
+        if mode == "carried_api":
+            carrier = CarriedChecker(THREADS)
+            handles = []
+            for i in range(depth):
+                layer = layers[i % len(layers)]
+                outs = {}
+                for _, names in LAUNCHES:
+                    outs.update(zip(names, carrier.gemv_group(pairs(layer, names))))
+                handles.extend(carrier.check_many([(layer[n]["bank"][BLOCK], layer[n]["x"], outs[n])
+                                                   for n, _, _ in LAYER]))  # fmt: skip
+            carrier.flush()
+            return [h.result() for h in handles]
         if mode.startswith(("carried", "inpass")):
             block = 256 if mode.endswith("_b256") else BLOCK
             return carried_pass(layers, depth, block, mode.startswith("inpass"), mode != "inpass_sums",
@@ -1184,6 +1202,7 @@ def main() -> None:
         o = sec["overhead_pct"]
         return {"inpass_b128": o["inpass"], "inpass_b256": o["inpass_b256"],
                 "bank_carried_b128": o["carried"], "bank_carried_b256": o["carried_b256"],
+                "bank_carried_check_many_b128": o["carried_api"],
                 "bank_serial_b128": o["serial"], "bank_side_stream_b128": o["side_stream"],
                 "inpass_sums_only": o["inpass_sums"]}  # fmt: skip
 

@@ -651,3 +651,138 @@ class SideStreamChecker:
     def wait_all(self) -> None:
         """Make the current stream wait for every check submitted so far."""
         torch.cuda.current_stream(self.stream.device).wait_stream(self.stream)
+
+
+def carry_selection(checker_ids: Sequence[int], limit: int = MAX_BATCH) -> list[int]:
+    """Positions of the queued checks one launch takes, oldest first: at most ``limit``, each
+    checker at most once (a launch takes a checker's descriptor once, as `check_many`
+    requires); a checker's later checks wait for a later launch."""
+    taken: list[int] = []
+    seen: set[int] = set()
+    for i, cid in enumerate(checker_ids):
+        if len(taken) == limit:
+            break
+        if cid not in seen:
+            seen.add(cid)
+            taken.append(i)
+    return taken
+
+
+class CarriedCheck:
+    """A check queued on a `CarriedChecker`.  Its `CheckResult` exists once a launch has taken
+    the check (a carrying GEMV launch or `CarriedChecker.flush`); the tensors fill in stream
+    order, as every result of this module does."""
+
+    def __init__(self) -> None:
+        self._result: CheckResult | None = None
+
+    @property
+    def launched(self) -> bool:
+        """Whether a launch has taken the check (its result tensors exist)."""
+        return self._result is not None
+
+    def result(self) -> CheckResult:
+        """The check's result; raises if no launch has taken the check yet."""
+        if self._result is None:
+            raise RuntimeError(
+                "the check has not been launched: issue a carrying GEMV launch through its "
+                "CarriedChecker or call flush()"
+            )
+        return self._result
+
+
+class CarriedChecker:
+    """The reference's call pattern, GEMV launches and then `check_many` over their outputs
+    (reference `src/pck/cuda/checker.py:143-171`), with the checks carried by later GEMV
+    launches instead of a launch of their own.
+
+    - `check_many(items)` (or `submit(checker, x, y)`) validates the checks and queues them;
+      it returns one `CarriedCheck` per item.
+    - `gemv_group(pairs)` (and `gemv_group_fp8_scaled(triples)`) issues the GEMVs.  A launch
+      of at least ``min_rows`` rows also carries up to eight queued checks, oldest first
+      (`pck_gemv_group_check`): its first workgroups run them while the rest stream the
+      weights.  Smaller launches carry nothing: a launch that fits in one round of the GPU
+      would wait for the CUs that host checks.
+    - `flush()` runs whatever is still queued as standalone launches (`check_many`).
+
+    Results are bit-identical to `check_many` on the same items.  A queued check's y must come
+    from a launch issued earlier on the stream that carries it: the stream current at
+    `submit` is recorded, and a launch on another stream refuses to carry the check.  Under
+    graph capture the queue is host state of the capture, as every launch argument is.  No
+    reference counterpart: the reference's checks are always a launch of their own.
+    """
+
+    def __init__(self, threads: int = 256, min_rows: int = 16384) -> None:
+        self.threads = threads
+        self.min_rows = min_rows
+        self._queue: list[tuple[tuple[GpuBlockedChecker, torch.Tensor, torch.Tensor], CarriedCheck, torch.cuda.Stream]] = []  # fmt: skip
+
+    @property
+    def pending(self) -> int:
+        """Checks queued and not yet launched."""
+        return len(self._queue)
+
+    def submit(self, checker: GpuBlockedChecker, x: torch.Tensor, y: torch.Tensor) -> CarriedCheck:
+        """Queue one check of output ``y`` for input ``x``."""
+        device = checker.c.device
+        _check_tensor(x, "x", torch.bfloat16, device)
+        _check_tensor(y, "y", torch.float32, device)
+        if x.dim() != 1 or x.size(0) != checker.n:
+            raise RuntimeError("x must have shape (n,)")
+        if y.dim() != 1 or y.size(0) != checker.num_blocks * checker.block:
+            raise RuntimeError("y must have shape (nb * b,)")
+        handle = CarriedCheck()
+        self._queue.append(((checker, x, y), handle, torch.cuda.current_stream(device)))
+        return handle
+
+    def check_many(
+        self, items: Sequence[tuple[GpuBlockedChecker, torch.Tensor, torch.Tensor]]
+    ) -> list[CarriedCheck]:
+        """Queue ``(checker, x, y)`` items (`check_many`'s arguments)."""
+        return [self.submit(checker, x, y) for checker, x, y in items]
+
+    def _take(self, rows: int, device: torch.device) -> list[tuple[Any, CarriedCheck, torch.cuda.Stream]]:  # fmt: skip
+        if rows < self.min_rows or not self._queue:
+            return []
+        picked = [self._queue[i] for i in carry_selection([id(e[0][0]) for e in self._queue])]
+        stream = torch.cuda.current_stream(device)
+        if any(e[2] != stream for e in picked):
+            raise RuntimeError("a queued check was submitted on another stream than this launch's")
+        return picked
+
+    def _settle(self, picked: list[tuple[Any, CarriedCheck, Any]], results: Sequence[CheckResult]) -> None:  # fmt: skip
+        for entry, result in zip(picked, results, strict=True):
+            entry[1]._result = result
+        taken = {id(e) for e in picked}
+        self._queue = [e for e in self._queue if id(e) not in taken]
+
+    def gemv_group(self, pairs: Sequence[tuple[torch.Tensor, torch.Tensor]]) -> list[torch.Tensor]:
+        """`gemv_group(pairs)`, carrying queued checks when the launch is large enough."""
+        from pck.cuda.gemv import gemv_group_check
+
+        picked = self._take(sum(int(W.size(0)) for W, _ in pairs), pairs[0][0].device) if pairs else []
+        ys, results = gemv_group_check(pairs, [e[0] for e in picked], self.threads)
+        self._settle(picked, results)
+        return ys
+
+    def gemv_group_fp8_scaled(
+        self, triples: Sequence[tuple[torch.Tensor, torch.Tensor, torch.Tensor]]
+    ) -> tuple[list[torch.Tensor], list[torch.Tensor]]:
+        """`gemv_group_fp8_scaled(triples)` (z and y = s z), carrying queued checks when the
+        launch is large enough."""
+        from pck.cuda.gemv import gemv_group_fp8_scaled
+
+        picked = self._take(sum(int(Q.size(0)) for Q, _, _ in triples), triples[0][0].device) if triples else []  # fmt: skip
+        zs, ys, results = gemv_group_fp8_scaled(triples, [e[0] for e in picked], self.threads)
+        self._settle(picked, results)
+        return zs, ys
+
+    def flush(self) -> None:
+        """Run every queued check now, in standalone launches on the current stream."""
+        while self._queue:
+            picked = [self._queue[i] for i in carry_selection([id(e[0][0]) for e in self._queue])]
+            device = picked[0][0][0].c.device
+            stream = torch.cuda.current_stream(device)
+            if any(e[2] != stream for e in picked):
+                raise RuntimeError("a queued check was submitted on another stream than this launch's")
+            self._settle(picked, check_many([e[0] for e in picked]))

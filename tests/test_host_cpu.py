@@ -92,3 +92,14 @@ def test_round_up_bf16_overflow_and_errors() -> None:
         round_up_bf16(torch.tensor([1.0]))
 
 
+
+
+def test_carry_selection_takes_each_checker_once_oldest_first() -> None:
+    from pck.cuda.checker import carry_selection
+
+    assert carry_selection([]) == []
+    assert carry_selection([7, 7, 7]) == [0]
+    assert carry_selection([1, 2, 1, 3, 2, 4]) == [0, 1, 3, 5]
+    assert carry_selection(list(range(12))) == list(range(8))  # at most eight per launch
+    assert carry_selection([5, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14], 8) == [0, 2, 3, 4, 5, 6, 7, 8]
+    assert carry_selection([1, 2, 3], limit=2) == [0, 1]
