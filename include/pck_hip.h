@@ -174,7 +174,9 @@ typedef struct PckCheckBatch {
 /* One launch checks every described output, one work item (a 256-lane workgroup) per
  * (check, block) pair: start[g + 1] - start[g] = checks * num_blocks.  The scratch fields
  * (partial_cx, partial_s, counters) and `segments` keep the reference's descriptor; the
- * kernel reads and writes neither (counters stay zero). */
+ * kernel reads and writes neither (counters stay zero).  With more pairs than compute units
+ * the launch deals the descriptors in another order (the longest rows where no second-round
+ * workgroup joins them); each descriptor's results do not depend on the order. */
 int pck_blocked_check(const PckCheckBatch* batch, void* stream);
 
 /* ---------------------------------------------------------------------------------------------

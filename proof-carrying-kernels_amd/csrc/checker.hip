@@ -56,13 +56,77 @@ __global__ void __launch_bounds__(kRowSumWaves * rowsum::kWave)
 }  // namespace
 }  // namespace pck
 
+namespace pck {
+namespace {
+
+// Compute units of the current device, looked up once per device.
+int compute_units() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 0;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+// Dispatch order of a launch with more (check, block) pairs than compute units.  The
+// dispatcher deals workgroups to the XCDs in turn and to each XCD's CUs in order, so the pairs
+// past the first round land on the CUs of the first (pairs - CUs) ones, which then run two.
+// The descriptor with the longest rows (down's, 14,336 columns in a Llama layer) goes right
+// after enough descriptors to cover those pairs, on CUs of its own; the others keep their
+// order.  Each pair writes only its own outputs, so every bit is unchanged: measured on the
+// Llama-3-8B layer's standalone check, 9.16% against 9.58% (BF16) and 13.9% against 15.0%
+// (FP8) of the layer, same box, three alternating rounds.
+PckCheckBatch dispatch_order(const PckCheckBatch& in) {
+  const int count = in.count;
+  const int64_t items = in.start[count];
+  const int cus = compute_units();
+  int longest = 0;
+  bool uneven = false;
+  for (int g = 1; g < count; ++g) {
+    uneven = uneven || in.desc[g].n != in.desc[0].n;
+    if (in.desc[g].n > in.desc[longest].n) longest = g;
+  }
+  if (count < 2 || !uneven || cus <= 0 || items <= cus) return in;
+  int order[PCK_MAX_BATCH];
+  int placed = 0;
+  int64_t covered = 0;
+  for (int g = 0; g < count; ++g) {  // the prefix that takes the second round's CUs
+    if (g == longest || covered >= items - cus) continue;
+    order[placed++] = g;
+    covered += in.start[g + 1] - in.start[g];
+  }
+  order[placed++] = longest;
+  for (int g = 0; g < count; ++g) {
+    bool taken = false;
+    for (int i = 0; i < placed; ++i) taken = taken || order[i] == g;
+    if (!taken) order[placed++] = g;
+  }
+  PckCheckBatch out = in;
+  out.start[0] = 0;
+  for (int i = 0; i < count; ++i) {
+    const int g = order[i];
+    out.desc[i] = in.desc[g];
+    out.start[i + 1] = out.start[i] + (in.start[g + 1] - in.start[g]);
+  }
+  return out;
+}
+
+}  // namespace
+}  // namespace pck
+
 extern "C" int pck_blocked_check(const PckCheckBatch* batch, void* stream) {
   if (batch == nullptr || pck::check::validate(*batch) != hipSuccess) return hipErrorInvalidValue;
   const int64_t items = batch->start[batch->count];
   if (items * pck::check::kThreads > 0xFFFFFFFFll)
     return hipErrorInvalidValue;  // the dispatch size is 32-bit in work-items
+  const PckCheckBatch ordered = pck::dispatch_order(*batch);
   pck::blocked_check_kernel<<<dim3(static_cast<unsigned>(items)), dim3(pck::check::kThreads), 0,
-                              static_cast<hipStream_t>(stream)>>>(*batch);
+                              static_cast<hipStream_t>(stream)>>>(ordered);
   return hipGetLastError();
 }
 

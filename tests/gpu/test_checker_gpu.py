@@ -294,6 +294,32 @@ def test_batch_matches_individual_checks() -> None:
         assert res.verdict.all()
 
 
+def test_a_launch_with_more_pairs_than_cus_keeps_every_result() -> None:
+    # 128 + 128 + 32 + 16 (check, block) pairs over uneven row lengths: more than the GPU's
+    # compute units, so the launch deals the longest rows in another order.
+    shapes = [(16384, 512), (16384, 512), (4096, 2048), (2048, 512)]
+    gen = torch.Generator().manual_seed(21)
+    items = []
+    for m, n in shapes:
+        W = (torch.randn(m, n, generator=gen) * 0.02).to(torch.bfloat16).cuda()
+        x = torch.randn(n, generator=gen).to(torch.bfloat16).cuda()
+        ch = GpuBlockedChecker(W, 128, tree_height(n, THREADS, vec=8), generator=gen)
+        items.append((ch, x, gemv_coalesced(W, x, THREADS)))
+    pairs = sum(ch.num_blocks * ch.checks for ch, _, _ in items)
+    assert pairs > torch.cuda.get_device_properties(0).multi_processor_count
+    y_bad = items[2][2].clone()
+    y_bad[5] += 1.0  # one block of the longest rows fails, and only that one
+    items[2] = (items[2][0], items[2][1], y_bad)
+    for (checker, x, y), res in zip(items, check_many(items), strict=True):
+        alone = checker.check(x, y)  # one descriptor: launched in its own order
+        assert torch.equal(res.passed, alone.passed)
+        assert torch.equal(res.rho, alone.rho)
+        assert torch.equal(res.tau, alone.tau)
+    verdicts = [r.verdict for r in check_many(items)]
+    assert all(bool(v.all()) for i, v in enumerate(verdicts) if i != 2)
+    assert verdicts[2].tolist() == [False] + [True] * (len(verdicts[2]) - 1)
+
+
 def test_more_than_one_launch_and_fault_isolation() -> None:
     items = [make_item(*CONFIGS[i % len(CONFIGS)], seed=10 + i) for i in range(11)]
     checker, x, y = items[9]
