@@ -5,7 +5,9 @@
 // per column) and its b outputs, and decides the verdict alone.  There is no communication
 // between workgroups: MI355X has one L2 per XCD, and publishing partial sums across workgroups
 // needs an agent-scope release / acquire, an L2 write-back and invalidate per workgroup, which
-// costs far more than the few KiB each pair reads.  A layer's 300+ pairs fill the 256 CUs.
+// costs far more than the few KiB each pair reads.  A layer's 300+ pairs fill the 256 CUs;
+// with more pairs than CUs the launch deals the longest-row descriptor where no second-round
+// workgroup joins it (dispatch_order below).
 //
 // The descriptor's scratch (partial sums, counters) and `segments` keep the reference's ABI
 // (src/pck/cuda/csrc/checker.h:13-44); this kernel reads and writes neither, and counters stay
