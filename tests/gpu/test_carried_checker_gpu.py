@@ -163,3 +163,18 @@ def test_carried_checker_in_a_graph() -> None:
         for a, b in zip(captured, eager):
             same(a, b)
             assert a.verdict.all()
+
+
+def test_other_thread_counts_run_the_checks_before_the_gemvs() -> None:
+    # At threads != 256 the carried checks run as their own launch just before the GEMVs
+    # (same results); the carrying GEMVs keep their own bits at that thread count.
+    produced = weights(SHAPES, seed=13)
+    big = weights([CARRIER], seed=14)[0]
+    carrier = CarriedChecker(threads=128, min_rows=4096)
+    ys = [gemv_group([(W, x)])[0] for W, x, _ in produced]
+    items = [(ch, x, y) for (W, x, ch), y in zip(produced, ys)]
+    hs = carrier.check_many(items)
+    out = carrier.gemv_group([(big[0], big[1])])[0]
+    for h, alone in zip(hs, check_many(items)):
+        same(h.result(), alone)
+    assert torch.equal(out.view(torch.int32), gemv_group([(big[0], big[1])], 128)[0].view(torch.int32))
