@@ -152,8 +152,11 @@ __device__ __forceinline__ double bf16_hi(uint32_t w) { return __uint_as_float(w
 
 // max(|v|, 2^-126) for eight packed BF16 values (0x0080 is 2^-126).
 __device__ __forceinline__ bf16x8 abs_floor8(u32x4 v) {
-  const u16x8 h = __builtin_bit_cast(u16x8, v & 0x7FFF7FFFu);
-  const u16x8 f = __builtin_elementwise_max(h, (u16x8)(0x80));
+  u32x4 a = v & 0x7FFF7FFFu;
+  // the AND stays one 32-bit instruction per pair (without the empty asm the compiler splits
+  // it per 16-bit value and repacks)
+  __asm__("" : "+v"(a));
+  const u16x8 f = __builtin_elementwise_max(__builtin_bit_cast(u16x8, a), (u16x8)(0x80));
   return __builtin_bit_cast(bf16x8, f);
 }
 
